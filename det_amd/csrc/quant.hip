@@ -1,0 +1,150 @@
+// Activation quantization kernels: det_quant, det_rmsnorm_quant, det_silu_mul_quant.
+// One workgroup (4 waves of 64) per row; the row is staged in LDS as fp32 so any n works with one code path.
+// Semantics are those of the reference backend (crates/det/src/cpu.rs:105-140,187-211 over
+// spec/quant.rs:8-49), including Rust's casts: a NaN multiplier (0/0 when sx underflows to 0) becomes 0 and a NaN
+// code becomes 0.
+#include <string.h>
+#include "common.h"
+#include "../../include/det_hip.h"
+using namespace det;
+
+namespace {
+
+constexpr int QT = 256;            // threads per row
+constexpr int QW = QT / 64;        // waves per row
+
+enum { MODE_QUANT = 0, MODE_RMSNORM = 1, MODE_SILU_MUL = 2 };
+
+__host__ __device__ __forceinline__ int p_of(int n) { int p = 1; while (p < n) p <<= 1; return p; }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmax_spec(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// dynamic LDS: v[n] fp32 (the row after its producer op), then for MODE_RMSNORM the tree buffers s[p], t[p/2]
+template <int MODE>
+__global__ void __launch_bounds__(QT) k_quant(const float* __restrict__ a, const float* __restrict__ b, float eps, int n,
+                                              float* __restrict__ y, int8_t* __restrict__ xq, float* __restrict__ sx,
+                                              uint16_t* __restrict__ mx) {
+    extern __shared__ float lds[];
+    __shared__ float red[QW];
+    __shared__ float sg[1024];
+    float* v = lds;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const size_t off = (size_t)row * n;
+
+    for (int i = tid; i < n; i += QT) {
+        float x = a[off + i];
+        if (MODE == MODE_SILU_MUL) {
+            x = silu_f(x) * b[off + i];
+            if (y) y[off + i] = x;
+        }
+        v[i] = x;
+    }
+    if (MODE == MODE_RMSNORM) {
+        // spec/prim.rs:172-181: ss = treesum(x*x) over the row padded with +0 to p = next power of two
+        float* s = lds + n;            // ping-pong tree buffers s[p], t[p/2]
+        float* t = s + p_of(n);
+        const int p = p_of(n);
+        __syncthreads();
+        for (int i = tid; i < p; i += QT) s[i] = i < n ? v[i] * v[i] : 0.0f;
+        for (int w = p >> 1; w >= 1; w >>= 1) {
+            __syncthreads();
+            for (int i = tid; i < w; i += QT) t[i] = s[2 * i] + s[2 * i + 1];
+            float* u = s; s = t; t = u;
+        }
+        __syncthreads();
+        const float ss = s[0];
+        const float mean = ss / (float)n;
+        const float inv = 1.0f / __builtin_sqrtf(mean + eps);
+        for (int i = tid; i < n; i += QT) {
+            const float t = (v[i] * inv) * b[i];
+            v[i] = t;
+            if (y) y[off + i] = t;
+        }
+    }
+    __syncthreads();
+    if (!xq) return;
+
+    if (mx) {
+        // spec/quant.rs:21-49
+        const int G = n / GROUP;
+        for (int g = wv; g < G; g += QW) {
+            const float am = wave_max(fmax_spec(__builtin_fabsf(v[g * GROUP + lane]), __builtin_fabsf(v[g * GROUP + 64 + lane])));
+            if (lane == 0) sg[g] = am / 127.0f;
+        }
+        __syncthreads();
+        float smax = 0.0f;
+        for (int g = 0; g < G; g++) smax = fmax_spec(smax, sg[g]);
+        const float s = smax == 0.0f ? 1.0f : smax / 65535.0f;
+        for (int g = wv; g < G; g += QW) {
+            float m = rint_(sg[g] / s);
+            if (m < 1.0f) m = 1.0f;
+            else if (m > 65535.0f) m = 65535.0f;
+            const unsigned int mi = __builtin_isnan(m) ? 0u : (unsigned int)m;
+            const float inv = 1.0f / (s * (float)mi);
+            int8_t* q = xq + off + g * GROUP;
+            q[lane] = (int8_t)clamp_i8(rint_(v[g * GROUP + lane] * inv));
+            q[64 + lane] = (int8_t)clamp_i8(rint_(v[g * GROUP + 64 + lane] * inv));
+            if (lane == 0) mx[(size_t)row * G + g] = (uint16_t)mi;
+        }
+        if (tid == 0) sx[row] = s;
+    } else {
+        // spec/quant.rs:8-16 quant_act_i8 over the whole row
+        float am = 0.0f;
+        for (int i = tid; i < n; i += QT) am = fmax_spec(am, __builtin_fabsf(v[i]));
+        am = wave_max(am);
+        if (lane == 0) red[wv] = am;
+        __syncthreads();
+        am = 0.0f;
+        for (int w = 0; w < QW; w++) am = fmax_spec(am, red[w]);
+        const float s = am == 0.0f ? 1.0f : am / 127.0f;
+        const float inv = 1.0f / s;
+        for (int i = tid; i < n; i += QT) xq[off + i] = (int8_t)clamp_i8(rint_(v[i] * inv));
+        if (tid == 0) sx[row] = s;
+    }
+}
+
+template <int MODE>
+void launch(const float* a, const float* b, float eps, int M, int n, float* y, int8_t* xq, float* sx, uint16_t* mx,
+            hipStream_t st, const char* who) {
+    if (M < 1) return;
+    if (n < 1) DET_FAIL("%s: bad n=%d", who, n);
+    if (mx && (n % GROUP)) DET_FAIL("%s: group mode needs n %% 128 == 0 (n=%d)", who, n);
+    if (n / GROUP > 1024) DET_FAIL("%s: n=%d exceeds 1024 groups", who, n);
+    int p = 1;
+    while (p < n) p <<= 1;
+    if (MODE == MODE_RMSNORM && p > 8192) DET_FAIL("%s: unsupported n=%d", who, n);
+    const size_t lds = (size_t)n * 4 + (MODE == MODE_RMSNORM ? (size_t)p * 6 : 0);
+    if (lds > 150 * 1024) DET_FAIL("%s: row of n=%d does not fit in LDS", who, n);
+    static bool attr = false;
+    if (!attr) {
+        DET_CHECK(hipFuncSetAttribute((const void*)k_quant<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024));
+        attr = true;
+    }
+    k_quant<MODE><<<M, QT, lds, st>>>(a, b, eps, n, y, xq, sx, mx);
+    DET_CHECK(hipGetLastError());
+}
+
+} // namespace
+
+extern "C" {
+
+void det_quant(const float* x, int M, int n, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st) {
+    if (!xq || !sx) DET_FAIL("det_quant: xq and sx are required");
+    launch<MODE_QUANT>(x, nullptr, 0.0f, M, n, nullptr, xq, sx, mx, st, "det_quant");
+}
+
+void det_rmsnorm_quant(const float* x, const float* w, float eps, int M, int n, float* y, int8_t* xq, float* sx, uint16_t* mx,
+                       hipStream_t st) {
+    launch<MODE_RMSNORM>(x, w, eps, M, n, y, xq, sx, mx, st, "det_rmsnorm_quant");
+}
+
+void det_silu_mul_quant(const float* g, const float* u, int M, int n, float* h, int8_t* hq, float* sh, uint16_t* mh,
+                        hipStream_t st) {
+    launch<MODE_SILU_MUL>(g, u, 0.0f, M, n, h, hq, sh, mh, st, "det_silu_mul_quant");
+}
+
+} // extern "C"

@@ -1,0 +1,90 @@
+// det_hip.h -- C API of det's quantized-linear path on AMD Instinct MI355X (gfx950, HIP).
+//
+// Drop-in for the GEMM / activation-quantization / runtime part of det's CUDA C API
+// (reference kernels/cuda/det_cuda.h).  Names, argument meaning and error behaviour are the same; the
+// only type change is hipStream_t for cudaStream_t, and det_hip_stream for det_cuda_stream.
+//   * every pointer is a DEVICE pointer (det_malloc); the host moves data with det_memcpy;
+//   * hipStream_t 0 (the null stream) is the one in-order stream; det_sync waits for the whole device;
+//   * compute calls return nothing: an invalid shape prints a message and aborts, as in the reference.
+// Row-major layouts, fp32 unless noted.
+#pragma once
+#include <stdint.h>
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// ---- runtime (replaces kernels/cuda/runtime.cu; declarations of det_cuda.h:15-24)
+int         det_init(void);                 // selects the current device; 0 on success (called lazily otherwise)
+const char* det_device_name(void);
+void*       det_malloc(size_t bytes);       // zero-initialised device buffer; NULL on failure
+void        det_free(void* p);              // waits for pending work first; aborts on a pointer det_malloc did not return
+size_t      det_allocated_bytes(void);
+void        det_sync(void);                 // wait for all pending GPU work (aborts on a kernel error)
+void        det_flush(void);                // no-op (launches are already submitted)
+void        det_memset(void* p, int value, size_t bytes, hipStream_t st);
+void        det_memcpy(void* dst, const void* src, size_t bytes, hipStream_t st);   // any direction (hipMemcpyDefault)
+void*       det_hip_stream(void);           // the stream det's work runs on (det_cuda_stream, det_cuda.h:24)
+
+// ---- weights: a quantized linear y = W x, W[N][K] (spec §2; det_cuda.h:27-32)
+// Same struct as det_cuda.h.  The pointers hold the HIP layout that det_linear_repack writes (the layout is
+// private to this backend, as the Metal backend's tiled codes are to it):
+//   wq: packed codes in 64-row tiles, [ceil(N/64)][K/128][GB/16][64 rows][16 bytes], where GB = 128, 96, 64 bytes
+//       is one row's packed 128-group (4 * bytes_per_32) for W8, W6, W4; the 16-byte chunk c of a tile row is bytes
+//       [16c, 16c+16) of that row's packed group, exactly as in the det row; rows past N are zero;
+//   c:  [ceil(N/64)*64] fp32 (zero past N);
+//   m:  [ceil(N/64)][K/128][64] uint16 (zero past N).
+typedef struct {
+    const uint8_t* wq;
+    const float*   c;
+    const uint16_t* m;
+    int N, K, bits;      // bits in {4,6,8}
+} det_qlinear;
+
+// Sizes of the three planes of det_linear_repack for an N x K linear of `bits`.
+// Replaces the row split of the CUDA backend's Backend::linear (reference crates/det/src/cuda.rs:139-163).
+void det_linear_sizes(int N, int K, int bits, size_t* wq_bytes, size_t* c_bytes, size_t* m_bytes);
+// Load-time repack: `rows` are N det rows ([codes][c fp32][m u16 x K/128], spec/tensor.rs:49-70, the GGUF tensor
+// data; several tensors fused along N are simply consecutive rows) in device memory; writes the three planes.
+void det_linear_repack(const uint8_t* rows, int N, int K, int bits, uint8_t* wq, float* c, uint16_t* m, hipStream_t st);
+
+// Weight quantizer: N rows of K fp32 weights (device) -> N det rows (device), bit-identical to det convert's
+// quantize_rows (reference crates/det/src/quantize.rs:33-100): per 128-group the best of 11 scales by binary64
+// squared error, c = f32(max_g s_g / 65535), m_g = rint(s_g / c), wq = rint(w / (c * m_g)).
+void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hipStream_t st);
+
+// ---- glue (replaces kernels/cuda/norm.cu; det_cuda.h:35-42)
+// Activation quantization (spec quant_act_i8g): per row sx[M] fp32 and, if mx != NULL, per-(row, 128-group)
+// multipliers mx[M][n/128] uint16 (n must be a multiple of 128); if mx == NULL, plain per-row int8 (quant_act_i8).
+void det_quant(const float* x, int M, int n, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st);
+// x[M][n] -> y[M][n] = rmsnorm(x,w,eps) (y may be NULL) and, if xq != NULL, quantize y into xq[M][n], sx, mx
+void det_rmsnorm_quant(const float* x, const float* w, float eps, int M, int n, float* y, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st);
+// h = silu(g)*u (h may be NULL) + quant
+void det_silu_mul_quant(const float* g, const float* u, int M, int n, float* h, int8_t* hq, float* sh, uint16_t* mh, hipStream_t st);
+
+// ---- GEMM (replaces kernels/cuda/gemm.cu; det_cuda.h:45-57)
+//      y[M][N] = ((float)acc * c[n]) * sx[m],  acc = sum_g (m[n,g]*mx[m,g]) * sum_{k in g} wq[n,k]*xq[m,k]
+//      mx[M][K/128] uint16 (NULL = all ones).  acc exact in int64.  accumulate != 0: y += result.  nparts > 1: the
+//      output columns are routed into nparts buffers (part i = columns [offs[i], offs[i+1]), offs[0] == 0, dsts[i] is
+//      [M][width_i]; y unused).  M < 1 is a no-op.  K % 128 != 0, N < 1, nparts > 4, offs[0] != 0, y == NULL
+//      (with nparts <= 1) or bits not in {4,6,8}: message on stderr and abort().
+void det_gemm(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, hipStream_t st);
+void det_gemm_ex(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, int accumulate,
+                 int nparts, const int* offs, float* const* dsts, hipStream_t st);
+// Scratch (det_cuda.h:52-57).  The HIP kernels keep their split-K partial sums in a buffer the library owns;
+// a caller-provided buffer of at least det_gemm_scratch_bytes(M, K) bytes is accepted for compatibility and
+// kept registered, and is never required.
+size_t det_gemm_scratch_bytes(int M, int K);
+void det_gemm_set_scratch(void* p, size_t bytes);
+
+// ---- test hooks (replaces det_test_prim of runtime.cu; det_cuda.h:114-118): elementwise fp32 primitives on arrays,
+// for bit-exactness tests vs the spec.
+// op: 0 exp_f, 1 log_f, 2 softplus_f, 3 sigmoid_f, 4 silu_f, 5 i64->f32 of (long long) bits of x pairs (x[2i],x[2i+1]),
+//     6 rint, 7 1/x, 8 sqrt, 9 x*y (y = x reversed), 10 x+y, 11 treesum of each row of n (out[M]), 12 native i64->f32,
+//     13 rint as int, 14 x/y, 15 x-y, 16 max(x,y)
+void det_test_prim(int op, const float* x, int M, int n, float* out, hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
