@@ -1,0 +1,215 @@
+"""Benchmark of det's quantized-linear path on one MI355X (BASELINE.json metric and configs).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (the prefill config; configs[0] rides along as the decode line):
+  * step = one W6 x int8 GEMM, K=2560 -> N=9728, M=512 tokens (det_gemm_ex, GemmOut::Write), weights seeded
+    N(0, 0.02) quantized by det's rules on the device (det_quantize_rows), activations N(0,1) with every 37th row
+    x1e-3 and one all-zero row quantized by det_quant.  `value` = int8 TOPS (2*M*N*K per step).
+  * the other configs[1] shapes (W6 M=64, W8 head K=2560 -> N=248320 at M=1 and 512) and configs[0] (W6 M=1 decode)
+    are timed the same way and reported under "shapes", decode lines in GB/s of algorithmic bytes.
+Inputs are resident in HBM before timing.  Each shape rotates over enough weight copies (> 512 MB in total) that
+no launch finds its weights in the 256 MB Infinity Cache.  Kernel time comes from HIP events on the null stream
+(the stream det's kernels run on) around the timed launches.
+The CPU baseline (rank 0, N=1) times the oracle's C GEMM (a port of the reference's scalar path) on a bounded
+sample of the same W6 M=512 workload.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from det_amd import ffi  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+ROTATE_BYTES = 600 << 20
+
+
+class HipEvents:
+    """hipEventRecord / hipEventElapsedTime on the null stream."""
+
+    def __init__(self):
+        self.h = ctypes.CDLL('libamdhip64.so')
+        self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        assert self.h.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e):
+        assert self.h.hipEventRecord(e, None) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.h.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.h.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+
+def row_bytes(bits, K):
+    return K // 32 * {8: 32, 6: 24, 4: 16}[bits] + 4 + 2 * (K // 128)
+
+
+def algo_bytes(N, K, M, bits):
+    """Algorithmic bytes of one GEMM: packed weights with c and m, xq, mx, sx, y (Write)."""
+    return N * row_bytes(bits, K) + M * K + 2 * M * (K // 128) + 4 * M + 4 * M * N
+
+
+def make_linear_copies(N, K, bits, seed, min_bytes):
+    """Quantize seeded N(0, 0.02) weights on the device and repack them into enough copies to exceed min_bytes."""
+    w = (np.random.default_rng(seed).standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    wd = ffi.Buf.upload(w)
+    del w
+    rows = ffi.quantize_rows(wd, N, K, bits)
+    wd.free()
+    one = N * row_bytes(bits, K)
+    copies = max(1, -(-min_bytes // one))
+    lins = [ffi.Linear(None, K, bits, rows_on_device=(rows, N)) for _ in range(copies)]
+    ffi.lib().det_sync()
+    rows.free()
+    return lins
+
+
+def make_acts(M, K, seed):
+    x = np.random.default_rng(seed).standard_normal((M, K), dtype=np.float32)
+    x[::37] *= np.float32(1e-3)
+    if M > 1:
+        x[M // 2] = 0.0
+    xb = ffi.Buf.upload(x)
+    xq, sx, mx = ffi.Buf((M, K), np.int8), ffi.Buf(M, np.float32), ffi.Buf((M, K // 128), np.uint16)
+    ffi.quant(xb, M, K, xq, sx, mx)
+    return xq, sx, mx
+
+
+def time_gemm(ev, lins, xq, sx, mx, M, y, steps, warmup):
+    for i in range(warmup):
+        ffi.gemm(lins[i % len(lins)], xq, sx, mx, M, write=y)
+    ffi.lib().det_sync()
+    a, b = ev.event(), ev.event()
+    t0 = time.perf_counter()
+    ev.record(a)
+    for i in range(steps):
+        ffi.gemm(lins[i % len(lins)], xq, sx, mx, M, write=y)
+    ev.record(b)
+    ms = ev.elapsed_ms(a, b)
+    ffi.lib().det_sync()
+    wall = time.perf_counter() - t0
+    return ms / steps, wall
+
+
+def shape_line(name, N, K, M, bits, ms):
+    ops = 2.0 * M * N * K
+    byt = algo_bytes(N, K, M, bits)
+    tops = ops / (ms * 1e-3) / 1e12
+    gbs = byt / (ms * 1e-3) / 1e9
+    ai = ops / byt
+    bound_tops = min(INT8_PEAK_TOPS, ai * HBM_PEAK_GBS / 1e3)
+    bound = 'hbm' if bound_tops < INT8_PEAK_TOPS else 'mfma'
+    return {'shape': name, 'bits': bits, 'M': M, 'N': N, 'K': K, 'us': round(ms * 1e3, 3), 'TOPS': round(tops, 2),
+            'GBps': round(gbs, 1), 'bound': bound,
+            'frac_of_bound': round((gbs / HBM_PEAK_GBS) if bound == 'hbm' else (tops / INT8_PEAK_TOPS), 4)}
+
+
+def cpu_baseline(target_s=12.0):
+    """Times the oracle's C GEMM (OpenMP over output rows) on a bounded row sample of the W6 M=512 workload."""
+    threads = min(os.cpu_count() or 1, 16)
+    os.environ.setdefault('OMP_NUM_THREADS', str(threads))
+    threads = int(os.environ['OMP_NUM_THREADS'])
+    import oracle
+    K, M, bits = 2560, 512, 6
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    x[::37] *= np.float32(1e-3)
+    x[M // 2] = 0.0
+    xq, sx, mx = oracle.quant(x)
+    n = 64
+    while True:
+        rows = oracle.quantize_rows((rng.standard_normal((n, K), dtype=np.float32) * np.float32(0.02)), bits)
+        t0 = time.perf_counter()
+        oracle.gemm(rows, n, K, bits, xq, sx, mx)
+        dt = time.perf_counter() - t0
+        if dt > target_s / 4 or n >= 9728:
+            break
+        n = min(9728, n * max(2, int(target_s / 4 / max(dt, 1e-3))))
+    tops = 2.0 * M * n * K / dt / 1e12
+    return {'value': round(tops, 5), 'unit': 'TOPS', 'cores': threads, 'kind': 'port',
+            'sample': f'oracle C GEMM (scalar restatement of crates/det/src/cpu.rs:142-185, OpenMP over rows), '
+                      f'W6 K=2560 M=512 on {n} of the 9728 output rows, {dt:.2f} s'}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=200)
+    ap.add_argument('--warmup', type=int, default=20)
+    ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--only-main', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py: this build measures one GPU only (the path shards along N with an all-gather of y; '
+              'no multi-GPU figure is produced)', file=sys.stderr)
+        sys.exit(2)
+
+    L = ffi.lib()
+    assert L.det_init() == 0
+    device = L.det_device_name().decode()
+    ev = HipEvents()
+    K, N6, NH = 2560, 9728, 248320
+
+    lin6 = make_linear_copies(N6, K, 6, 1, ROTATE_BYTES)
+    xq, sx, mx = make_acts(512, K, 2)
+    y = ffi.Buf((512, NH), np.float32)
+    ms, wall = time_gemm(ev, lin6, xq, sx, mx, 512, y, args.steps, args.warmup)
+    main_line = shape_line('w6_9728x2560', N6, K, 512, 6, ms)
+
+    shapes = [main_line]
+    if not args.only_main:
+        for M in (1, 64):
+            xq_m, sx_m, mx_m = make_acts(M, K, 3 + M)
+            msm, _ = time_gemm(ev, lin6, xq_m, sx_m, mx_m, M, y, max(args.steps, 200), args.warmup)
+            shapes.append(shape_line('w6_9728x2560', N6, K, M, 6, msm))
+        for l in lin6:
+            for b in (l.wq, l.c, l.m):
+                b.free()
+        linh = make_linear_copies(NH, K, 8, 4, ROTATE_BYTES)
+        for M in (1, 512):
+            xq_m, sx_m, mx_m = make_acts(M, K, 5 + M)
+            msm, _ = time_gemm(ev, linh, xq_m, sx_m, mx_m, M, y, max(10, args.steps // 10), max(2, args.warmup // 10))
+            shapes.append(shape_line('w8_head_248320x2560', NH, K, M, 8, msm))
+
+    tops = main_line['TOPS']
+    out = {
+        'metric': 'W6xint8 GEMM: decode HBM GB/s, prefill int8 TOPS (% roofline), 1 MI355X',
+        'value': tops, 'unit': 'TOPS', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+        'ms_per_step': round(ms, 6), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'int8xint6->int32/int64, fp32 epilogue', 'data': 'synthetic (seeded Gaussian weights/activations)',
+        'config': {'workload': 'BASELINE configs[1]: W6 prefill GEMM K=2560 N=9728 M=512 (det_gemm_ex Write)',
+                   'M': 512, 'N': N6, 'K': K, 'bits': 6, 'device': device},
+        'roofline': {'bound': 'mfma', 'achieved': tops, 'peak': INT8_PEAK_TOPS, 'unit': 'TFLOP/s',
+                     'frac': round(tops / INT8_PEAK_TOPS, 4), 'traffic': None,
+                     'kernel': 'k_mfma<6,128>', 'algorithmic_ops_per_launch': 2 * 512 * N6 * K},
+        'shapes': shapes,
+        'timed_wall_s': round(wall, 4),
+    }
+    dec = [s for s in shapes if s['M'] == 1]
+    if dec:
+        out['decode'] = {s['shape']: {'GBps': s['GBps'], 'frac_of_hbm_peak': s['frac_of_bound'], 'us': s['us']} for s in dec}
+    if not args.no_cpu:
+        out['cpu_baseline'] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

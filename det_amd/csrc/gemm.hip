@@ -9,12 +9,11 @@
 // GB/16 chunk planes of [64 rows][16 bytes], so one wave instruction loads 1 KB of contiguous bytes.
 //
 // Kernels (chosen by shape only, like the reference's gemm_bits, gemm.cu:1016-1023):
-//   k_decode<BITS,MP> (M <= 8): one wave per (64-row tile, slice of groups).  Lane = output row; the lane streams
-//       its row's packed groups with dwordx4 loads, unpacks to signed int8 words in registers, and dots them with
-//       the activations (uniform across the wave, so they are scalar loads) with v_dot4c_i32_i8.  The int32 group
-//       partial is scaled by m*mx into int64.  When the grid would not fill the chip the K range is split over
-//       waves; the partial int64 sums meet in a self-cleaning device buffer with atomics and the last wave of a
-//       tile runs the epilogue.
+//   k_decode<BITS,MP> (M <= 8): one workgroup per 64-row tile, lane = output row.  The lane streams its row's
+//       packed groups with dwordx4 loads, unpacks to signed int8 words in registers, and dots them with the
+//       activations (uniform across the wave, so they are scalar loads) with v_dot4c_i32_i8; the int32 group partial
+//       is scaled by m*mx into int64.  When the tiles alone would not fill the chip, the groups are split over up
+//       to 16 waves of the workgroup and the int64 partial sums are added in LDS.
 //   k_mfma<BITS,BM> (M > 8): 128-row x BM-token workgroup tile, 4 waves of (BM/2) x 64.  Per 128-group the
 //       activation tile and the unpacked (signed int8) weight tile are staged in LDS; v_mfma_i32_32x32x32_i8 gives
 //       the exact int32 group partials, which are scaled into int64 accumulators before the next group.
@@ -93,22 +92,25 @@ __device__ __forceinline__ void mac_s32_u32(long long& acc, int p, uint32_t s) {
 }
 
 // ------------------------------------------------------------------ decode (M <= 8)
+// One workgroup per 64-row tile with S waves; wave w takes the groups g = w, w + S, ...  The waves' exact int64
+// partial sums meet in LDS; wave w finishes tokens w, w + S, ...
+constexpr int DEC_MAXW = 16;
+
 template <int BITS, int MP>
-__global__ void __launch_bounds__(64) k_decode(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
+__global__ void __launch_bounds__(64 * DEC_MAXW) k_decode(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                 const uint16_t* __restrict__ ms, int N, int K,
                                                 const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                const uint16_t* __restrict__ mx, int M, Out out, int gps, int ks,
-                                                unsigned long long* __restrict__ part, unsigned int* __restrict__ cnt) {
+                                                const uint16_t* __restrict__ mx, int M, Out out) {
     constexpr int NC = group_bytes(BITS) / 16;     // 16-byte chunks per row-group
-    const int lane = threadIdx.x;
-    const int tile = blockIdx.x / ks, slice = blockIdx.x - tile * ks;
+    extern __shared__ long long red_dyn[];          // [S][MP][64] int64 partial sums
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, S = blockDim.x >> 6;
+    const int tile = blockIdx.x;
     const int G = K / GROUP;
-    const int g0 = slice * gps, g1 = min(G, g0 + gps);
     long long acc[MP];
 #pragma unroll
     for (int t = 0; t < MP; t++) acc[t] = 0;
 
-    for (int g = g0; g < g1; g++) {
+    for (int g = wv; g < G; g += S) {
         const size_t tg = (size_t)tile * G + g;
         const uint4* src = reinterpret_cast<const uint4*>(wq + tg * NC * 1024) + lane;
         uint32_t q[NC * 4];
@@ -120,7 +122,7 @@ __global__ void __launch_bounds__(64) k_decode(const uint8_t* __restrict__ wq, c
         const uint32_t mm = ms[tg * 64 + lane];
         uint32_t w[32];
 #pragma unroll
-        for (int b = 0; b < 4; b++) block_signed<BITS>(q + b * (NC), w + 8 * b);
+        for (int b = 0; b < 4; b++) block_signed<BITS>(q + b * NC, w + 8 * b);
 #pragma unroll
         for (int t = 0; t < MP; t++) {
             if (t < M) {
@@ -133,9 +135,8 @@ __global__ void __launch_bounds__(64) k_decode(const uint8_t* __restrict__ wq, c
             }
         }
     }
-
     const int n = tile * TILE_N + lane;
-    if (ks == 1) {
+    if (S == 1) {
         if (n < N) {
             const float c = cs[n];
 #pragma unroll
@@ -144,30 +145,16 @@ __global__ void __launch_bounds__(64) k_decode(const uint8_t* __restrict__ wq, c
         }
         return;
     }
-    // split-K: exact int64 partial sums meet in part[t][Npad]; the last wave of the tile finishes and clears them
-    const size_t npad = (size_t)gridDim.x / ks * TILE_N;
 #pragma unroll
-    for (int t = 0; t < MP; t++)
-        if (t < M)
-            __hip_atomic_fetch_add(part + (size_t)t * npad + n, (unsigned long long)acc[t], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
-    unsigned int last = 0;
-    if (lane == 0)
-        last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ks - 1);
-    last = __shfl(last, 0, 64);
-    if (!last) return;
-    __threadfence();
-    const float c = n < N ? cs[n] : 0.0f;
-#pragma unroll
-    for (int t = 0; t < MP; t++) {
-        if (t < M) {
-            const long long tot = (long long)__hip_atomic_exchange(part + (size_t)t * npad + n, 0ull, __ATOMIC_RELAXED,
-                                                                   __HIP_MEMORY_SCOPE_AGENT);
-            if (n < N) out.store(N, t, n, (i64_to_f(tot) * c) * sx[t]);
+    for (int t = 0; t < MP; t++) red_dyn[(wv * MP + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (n < N) {
+        for (int t = wv; t < M && t < MP; t += S) {
+            long long tot = 0;
+            for (int w = 0; w < S; w++) tot += red_dyn[(w * MP + t) * 64 + lane];
+            out.store(N, t, n, (i64_to_f(tot) * cs[n]) * sx[t]);
         }
     }
-    if (lane == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------ MFMA GEMM (M > 8)
@@ -280,6 +267,212 @@ __global__ void __launch_bounds__(256) k_mfma(const uint8_t* __restrict__ wq, co
                 const int t = t0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (t < M) out.store(N, t, n, (i64_to_f(acc[i][j][r]) * cn) * sx[t]);
             }
+    }
+}
+
+// ------------------------------------------------------------------ prefill MFMA GEMM (M > 64)
+// Workgroup tile 128 tokens x 128 rows, 4 waves of 64 x 64 (2 x 2 v_mfma_i32_32x32x32_i8 tiles), two workgroups
+// per CU.  Per 128-group: the next group's activations, packed codes and multipliers are loaded into registers
+// while the current group runs on the MFMA; the codes are then unpacked to signed int8 and both tiles are stored
+// to the other LDS buffer (one barrier per group).
+//
+// Group scaling with two VALU ops per (token, row, group): the first MFMA of a group starts from a constant
+// accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
+//     U += (p + B) * (m * mx)            (v_mul_u32_u24, v_mad_u64_u32; exact, U < 2^62)
+// The bias is removed once per output: acc = U - B * S with S = sum_g m[n,g] * mx[t,g], computed exactly on the
+// MFMA from balanced int8 digits v = 256*v1 + v0 + 32896 (v1, v0 in [-128, 127]) of m and mx:
+//     S = 65536*D11 + 256*(D10 + D01) + D00 + 32896*(Ra[t] + Rb[n]) + G*32896^2,
+//     Dij = sum_g a_i[t,g] b_j[n,g],  Ra[t] = sum_g (mx - 32896),  Rb[n] = sum_g (m - 32896).
+constexpr int PF_BM = 128, PF_BN = 128, PF_STR = 144;
+constexpr uint32_t PF_BIAS = 1u << 21;
+constexpr int DIG_C = 32896;
+
+__device__ __forceinline__ void digits16(uint32_t v, int& d1, int& d0) {
+    const int vp = (int)v - DIG_C;
+    d0 = ((vp + 128) & 255) - 128;
+    d1 = (vp - d0) >> 8;
+}
+
+template <int BITS>
+__global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
+                                                      const uint16_t* __restrict__ ms, int N, int K,
+                                                      const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                      const uint16_t* __restrict__ mx, int M, Out out) {
+    constexpr int NC = group_bytes(BITS) / 16;
+    __shared__ __attribute__((aligned(16))) int8_t As[2][PF_BM * PF_STR];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[2][PF_BN * PF_STR];
+    __shared__ __attribute__((aligned(16))) uint32_t mxs[2][PF_BM];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv >> 1, wn = wv & 1;
+    const int n0 = blockIdx.x * PF_BN, t0 = blockIdx.y * PF_BM;
+    const int G = K / GROUP;
+    const int tile0 = n0 / TILE_N;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    unsigned long long U[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) U[i][j][r] = 0;
+    v16i bias;
+#pragma unroll
+    for (int r = 0; r < 16; r++) bias[r] = (int)PF_BIAS;
+
+    // staging registers for one group
+    uint4 areg[4];
+    uint4 breg[NC / 2];
+    uint32_t mxreg = 1, mreg[2];
+    const int br = tid >> 1, bh = tid & 1;                     // weight staging: row br, half bh
+    const uint4* bsrc = reinterpret_cast<const uint4*>(wq + (size_t)(tile0 + (br >> 6)) * G * NC * 1024) + (br & 63);
+
+    auto load = [&](int g) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int ch = tid + i * 256, tl = ch >> 3, kc = ch & 7;
+            const int t = t0 + tl;
+            areg[i] = t < M ? *reinterpret_cast<const uint4*>(xq + (size_t)t * K + (size_t)g * GROUP + kc * 16)
+                            : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < NC / 2; c++) breg[c] = bsrc[((size_t)g * NC + bh * (NC / 2) + c) * 64];
+        if (tid < PF_BM) mxreg = (mx && t0 + tid < M) ? (uint32_t)mx[(size_t)(t0 + tid) * G + g] : 1u;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int nl = wn * 64 + j * 32 + l32;
+            mreg[j] = ms[((size_t)(tile0 + (nl >> 6)) * G + g) * 64 + (nl & 63)];
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int ch = tid + i * 256, tl = ch >> 3, kc = ch & 7;
+            *reinterpret_cast<uint4*>(&As[buf][tl * PF_STR + kc * 16]) = areg[i];
+        }
+        uint32_t q[NC * 2];
+#pragma unroll
+        for (int c = 0; c < NC / 2; c++) { q[4 * c] = breg[c].x; q[4 * c + 1] = breg[c].y; q[4 * c + 2] = breg[c].z; q[4 * c + 3] = breg[c].w; }
+        uint32_t w[16];
+        block_signed<BITS>(q, w);
+        block_signed<BITS>(q + NC, w + 8);
+        uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][br * PF_STR + bh * 64]);
+#pragma unroll
+        for (int c = 0; c < 4; c++) dst[c] = make_uint4(w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]);
+        if (tid < PF_BM) mxs[buf][tid] = mxreg;
+    };
+
+    load(0);
+    store(0);
+    uint32_t mcur[2] = {mreg[0], mreg[1]};
+    __syncthreads();
+    for (int g = 0; g < G; g++) {
+        const int buf = g & 1;
+        if (g + 1 < G) load(g + 1);
+        v16i d[2][2];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            v4i a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                a[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm * 64 + i * 32 + l32) * PF_STR + s * 32 + lh * 16]);
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                b[j] = *reinterpret_cast<const v4i*>(&Bs[buf][(wn * 64 + j * 32 + l32) * PF_STR + s * 32 + lh * 16]);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    d[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], s == 0 ? bias : d[i][j], 0, 0, 0);
+        }
+        // element (t, n) of a 32x32 tile: lane (n % 32) + 32 * ((t / 4) % 2), register 4 * (t / 8) + t % 4
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                const uint4 mv = *reinterpret_cast<const uint4*>(&mxs[buf][wm * 64 + i * 32 + 8 * q4 + 4 * lh]);
+                const uint32_t mxv[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const uint32_t sc = __umul24(mcur[j], mxv[e]);
+                        U[i][j][4 * q4 + e] += (unsigned long long)(uint32_t)d[i][j][4 * q4 + e] * sc;
+                    }
+            }
+        }
+        if (g + 1 < G) {
+            store(buf ^ 1);
+            mcur[0] = mreg[0];
+            mcur[1] = mreg[1];
+        }
+        __syncthreads();
+    }
+
+    // ---- bias correction: S = sum_g m * mx from balanced digits on the MFMA
+    __shared__ int Ra[PF_BM], Rb[PF_BN];
+    if (tid < PF_BM) {
+        const int t = t0 + tid;
+        int r = 0;
+        for (int g = 0; g < G; g++) r += (int)((mx && t < M) ? mx[(size_t)t * G + g] : 1u) - DIG_C;
+        Ra[tid] = r;
+    } else {
+        const int nl = tid - PF_BM;
+        int r = 0;
+        for (int g = 0; g < G; g++) r += (int)ms[((size_t)(tile0 + (nl >> 6)) * G + g) * 64 + (nl & 63)] - DIG_C;
+        Rb[nl] = r;
+    }
+    __syncthreads();
+    const long long GC2 = (long long)G * DIG_C * DIG_C;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int tl = wm * 64 + i * 32 + l32;            // A-operand row of this lane
+        const int ta = t0 + tl;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int nl = wn * 64 + j * 32 + l32;        // B-operand column of this lane (and output column)
+            const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+            v16i d11 = z, d10 = z, d01 = z, d00 = z;
+            for (int k0 = 0; k0 < G; k0 += 32) {
+                int a1[16], a0[16], b1[16], b0[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int g = k0 + lh * 16 + e;
+                    a1[e] = a0[e] = b1[e] = b0[e] = 0;
+                    if (g < G) {
+                        const uint32_t xv = (mx && ta < M) ? (uint32_t)mx[(size_t)ta * G + g] : 1u;
+                        digits16(xv, a1[e], a0[e]);
+                        const uint32_t mv = ms[((size_t)(tile0 + (nl >> 6)) * G + g) * 64 + (nl & 63)];
+                        digits16(mv, b1[e], b0[e]);
+                    }
+                }
+                v4i A1, A0, B1, B0;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    A1[w] = (a1[4 * w] & 255) | ((a1[4 * w + 1] & 255) << 8) | ((a1[4 * w + 2] & 255) << 16) | ((a1[4 * w + 3] & 255) << 24);
+                    A0[w] = (a0[4 * w] & 255) | ((a0[4 * w + 1] & 255) << 8) | ((a0[4 * w + 2] & 255) << 16) | ((a0[4 * w + 3] & 255) << 24);
+                    B1[w] = (b1[4 * w] & 255) | ((b1[4 * w + 1] & 255) << 8) | ((b1[4 * w + 2] & 255) << 16) | ((b1[4 * w + 3] & 255) << 24);
+                    B0[w] = (b0[4 * w] & 255) | ((b0[4 * w + 1] & 255) << 8) | ((b0[4 * w + 2] & 255) << 16) | ((b0[4 * w + 3] & 255) << 24);
+                }
+                d11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, d11, 0, 0, 0);
+                d10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, d10, 0, 0, 0);
+                d01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, d01, 0, 0, 0);
+                d00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, d00, 0, 0, 0);
+            }
+            const int n = n0 + nl;
+            const float cn = n < N ? cs[n] : 0.0f;
+            const long long rb = Rb[nl];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int tr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const long long S = 65536LL * d11[r] + 256LL * ((long long)d10[r] + d01[r]) + d00[r] +
+                                    (long long)DIG_C * ((long long)Ra[tr] + rb) + GC2;
+                const long long acc = (long long)(U[i][j][r] - ((unsigned long long)S << 21));
+                const int t = t0 + tr;
+                if (t < M && n < N) out.store(N, t, n, (i64_to_f(acc) * cn) * sx[t]);
+            }
+        }
     }
 }
 
@@ -397,50 +590,18 @@ __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ w, i
 int g_num_cus = 0;
 int g_decode_waves = 2048;      // target waves per decode launch (split-K below it)
 int g_decode_max_m = 8;
-
-// split-K buffers of k_decode: int64 partial sums [M][Npad] and per-tile arrival counters, zero between calls
-unsigned long long* g_part = nullptr;
-size_t g_part_cap = 0;          // elements
-unsigned int* g_cnt = nullptr;
-size_t g_cnt_cap = 0;
-void* g_user_scratch = nullptr;
+void* g_user_scratch = nullptr;     // registered for ABI compatibility; no HIP kernel needs it
 size_t g_user_scratch_bytes = 0;
-
-void ensure_split_buffers(size_t part_elems, size_t tiles, hipStream_t st) {
-    if (part_elems <= g_part_cap && tiles <= g_cnt_cap) return;
-    DET_CHECK(hipStreamSynchronize(st));     // earlier launches may still use the old buffers
-    if (part_elems > g_part_cap) {
-        if (g_part) DET_CHECK(hipFree(g_part));
-        g_part_cap = std::max(part_elems, (size_t)1 << 20);
-        DET_CHECK(hipMalloc(&g_part, g_part_cap * 8));
-        DET_CHECK(hipMemset(g_part, 0, g_part_cap * 8));
-    }
-    if (tiles > g_cnt_cap) {
-        if (g_cnt) DET_CHECK(hipFree(g_cnt));
-        g_cnt_cap = std::max(tiles, (size_t)1 << 14);
-        DET_CHECK(hipMalloc(&g_cnt, g_cnt_cap * 4));
-        DET_CHECK(hipMemset(g_cnt, 0, g_cnt_cap * 4));
-    }
-    DET_CHECK(hipDeviceSynchronize());
-}
 
 template <int BITS, int MP>
 void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
     const int G = L.K / GROUP;
     const int T = (L.N + TILE_N - 1) / TILE_N;
-    int gps = G, ks = 1;
-    if (T < g_decode_waves) {
-        gps = (int)std::max<long long>(1, ((long long)T * G) / g_decode_waves);
-        ks = (G + gps - 1) / gps;
-    }
-    unsigned long long* part = nullptr;
-    unsigned int* cnt = nullptr;
-    if (ks > 1) {
-        ensure_split_buffers((size_t)M * T * TILE_N, (size_t)T, st);
-        part = g_part;
-        cnt = g_cnt;
-    }
-    k_decode<BITS, MP><<<T * ks, 64, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, gps, ks, part, cnt);
+    // waves per tile: enough to put ~g_decode_waves waves in flight, at most one per group and DEC_MAXW
+    int S = (g_decode_waves + T - 1) / T;
+    S = std::max(1, std::min(S, std::min(G, DEC_MAXW)));
+    const size_t lds = S > 1 ? (size_t)S * MP * 64 * sizeof(long long) : 0;
+    k_decode<BITS, MP><<<T, 64 * S, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y);
     DET_CHECK(hipGetLastError());
 }
 
@@ -461,7 +622,9 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
     } else if (M <= 64) {
         launch_mfma<BITS, 64>(L, xq, sx, mx, M, y, st);
     } else {
-        launch_mfma<BITS, 128>(L, xq, sx, mx, M, y, st);
+        dim3 grid((L.N + PF_BN - 1) / PF_BN, (M + PF_BM - 1) / PF_BM);
+        k_prefill<BITS><<<grid, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y);
+        DET_CHECK(hipGetLastError());
     }
 }
 
