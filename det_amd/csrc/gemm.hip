@@ -34,16 +34,15 @@ struct Out {
     int acc, nparts;
     int offs[5];
     float* dst[4];
-    __device__ __forceinline__ void store(int N, int t, int n, float v) const {
-        float* p;
-        if (nparts <= 1) {
-            p = y + (size_t)t * N + n;
-        } else {
-            int i = 0;
+    __device__ __forceinline__ float* ptr(int N, int t, int n) const {
+        if (nparts <= 1) return y + (size_t)t * N + n;
+        int i = 0;
 #pragma unroll
-            for (int j = 1; j < 4; j++) if (j < nparts && n >= offs[j]) i = j;
-            p = dst[i] + (size_t)t * (offs[i + 1] - offs[i]) + (n - offs[i]);
-        }
+        for (int j = 1; j < 4; j++) if (j < nparts && n >= offs[j]) i = j;
+        return dst[i] + (size_t)t * (offs[i + 1] - offs[i]) + (n - offs[i]);
+    }
+    __device__ __forceinline__ void store(int N, int t, int n, float v) const {
+        float* p = ptr(N, t, n);
         *p = acc ? *p + v : v;
     }
 };
@@ -272,9 +271,11 @@ __global__ void __launch_bounds__(256) k_mfma(const uint8_t* __restrict__ wq, co
 
 // ------------------------------------------------------------------ prefill MFMA GEMM (M > 64)
 // Workgroup tile 128 tokens x 128 rows, 4 waves of 64 x 64 (2 x 2 v_mfma_i32_32x32x32_i8 tiles), two workgroups
-// per CU.  Per 128-group: the next group's activations, packed codes and multipliers are loaded into registers
-// while the current group runs on the MFMA; the codes are then unpacked to signed int8 and both tiles are stored
-// to the other LDS buffer (one barrier per group).
+// per CU.  LDS holds two buffers of the activation tile and of the signed int8 weight tile, 128 rows of 128 bytes
+// each, with the 16-byte chunk c of row r stored at position c ^ (r & 7) so that the fragment reads of 32 rows
+// spread over all banks.  Per 128-group, while the MFMAs run on one buffer, the next group's activations (and W8
+// codes) are copied global -> LDS by global_load_lds_dwordx4 into the other buffer; W4/W6 codes land in a packed
+// staging area that the same wave then unpacks into the other buffer (so one barrier per group suffices).
 //
 // Group scaling with two VALU ops per (token, row, group): the first MFMA of a group starts from a constant
 // accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
@@ -283,7 +284,7 @@ __global__ void __launch_bounds__(256) k_mfma(const uint8_t* __restrict__ wq, co
 // MFMA from balanced int8 digits v = 256*v1 + v0 + 32896 (v1, v0 in [-128, 127]) of m and mx:
 //     S = 65536*D11 + 256*(D10 + D01) + D00 + 32896*(Ra[t] + Rb[n]) + G*32896^2,
 //     Dij = sum_g a_i[t,g] b_j[n,g],  Ra[t] = sum_g (mx - 32896),  Rb[n] = sum_g (m - 32896).
-constexpr int PF_BM = 128, PF_BN = 128, PF_STR = 144;
+constexpr int PF_BM = 128, PF_BN = 128;
 constexpr uint32_t PF_BIAS = 1u << 21;
 constexpr int DIG_C = 32896;
 
@@ -292,20 +293,38 @@ __device__ __forceinline__ void digits16(uint32_t v, int& d1, int& d0) {
     d0 = ((vp + 128) & 255) - 128;
     d1 = (vp - d0) >> 8;
 }
+// byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+
+__device__ __forceinline__ void lds_load16(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
 
 template <int BITS>
 __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                       const uint16_t* __restrict__ ms, int N, int K,
                                                       const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                      const uint16_t* __restrict__ mx, int M, Out out) {
+                                                      const uint16_t* __restrict__ mx, int M, Out out, int nbn, int nbt) {
     constexpr int NC = group_bytes(BITS) / 16;
-    __shared__ __attribute__((aligned(16))) int8_t As[2][PF_BM * PF_STR];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[2][PF_BN * PF_STR];
-    __shared__ __attribute__((aligned(16))) uint32_t mxs[2][PF_BM];
+    constexpr int PK = BITS == 8 ? 16 : 2 * NC * 1024;         // packed staging bytes (W4/W6)
+    // Two buffers as distinct LDS objects, selected at compile time (the loop is unrolled by two), so that the
+    // compiler can see that reads of one buffer do not alias the global->LDS copies into the other and need not
+    // wait for them.
+    __shared__ __attribute__((aligned(16))) int8_t As0[PF_BM * 128], As1[PF_BM * 128];
+    __shared__ __attribute__((aligned(16))) int8_t Bs0[PF_BN * 128], Bs1[PF_BN * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t Bp[PK];
+    __shared__ __attribute__((aligned(16))) uint32_t mxs0[PF_BM], mxs1[PF_BM];   // mx[t][g] of the buffer's group
+    __shared__ __attribute__((aligned(16))) uint32_t mss0[PF_BN], mss1[PF_BN];   // m[n][g]
+    __shared__ int Ra[PF_BM], Rb[PF_BN];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv >> 1, wn = wv & 1;
-    const int n0 = blockIdx.x * PF_BN, t0 = blockIdx.y * PF_BM;
+    // XCD-aware tile order: consecutive workgroup ids go to different XCDs; give each XCD a contiguous run of
+    // tiles (row-block major) so that the token blocks sharing one weight tile run on the same L2.
+    int tile = blockIdx.x;
+    const int total = nbn * nbt;
+    if ((total & 7) == 0) tile = (tile & 7) * (total >> 3) + (tile >> 3);
+    const int n0 = (tile / nbt) * PF_BN, t0 = (tile % nbt) * PF_BM;
     const int G = K / GROUP;
     const int tile0 = n0 / TILE_N;
     const int l32 = lane & 31, lh = lane >> 5;
@@ -317,69 +336,91 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) U[i][j][r] = 0;
-    v16i bias;
-#pragma unroll
-    for (int r = 0; r < 16; r++) bias[r] = (int)PF_BIAS;
 
-    // staging registers for one group
-    uint4 areg[4];
-    uint4 breg[NC / 2];
-    uint32_t mxreg = 1, mreg[2];
-    const int br = tid >> 1, bh = tid & 1;                     // weight staging: row br, half bh
-    const uint4* bsrc = reinterpret_cast<const uint4*>(wq + (size_t)(tile0 + (br >> 6)) * G * NC * 1024) + (br & 63);
+    // weight copy: W8 straight into Bs (slot p = row r * 8 + position q takes chunk q ^ (r & 7) of row r),
+    // W4/W6 into the Bp planes (wave wv: tile wv >> 1, chunk planes (wv & 1) * NC/2 .. +NC/2, which are exactly
+    // the half-groups this wave unpacks itself).  Per-lane addresses are 32-bit offsets from uniform bases.
+    const uint8_t* wbase = wq + (size_t)tile0 * G * NC * 1024;
+    // per-group multipliers: thread tid < 128 stages mx of token t0 + tid, the others m of row n0 + tid - 128
+    // (branch-free: a thread whose multiplier is implicitly 1 reads a valid m entry and discards it)
+    const bool x_one = tid < PF_BM && !(mx && t0 + tid < M);
+    const uint16_t* s_ptr = (tid < PF_BM && !x_one) ? mx + (size_t)(t0 + tid) * G
+                                                    : ms + (size_t)((tile0 + ((tid & 127) >> 6)) * G) * 64 + (tid & 63);
+    const uint32_t s_step = (tid < PF_BM && !x_one) ? 1u : 64u;
+    uint32_t* const s_dst0 = tid < PF_BM ? mxs0 + tid : mss0 + (tid - PF_BM);
+    uint32_t* const s_dst1 = tid < PF_BM ? mxs1 + tid : mss1 + (tid - PF_BM);
+    uint32_t sreg = 1;
+    int rsum = 0;          // Ra (tid < 128) or Rb (tid >= 128): sum over groups of (multiplier - 32896)
 
-    auto load = [&](int g) {
+    // copy group g into (As, Bs / Bp) and its multiplier into sreg; nothing waits here
+    auto issue = [&](int g, int8_t* As, int8_t* Bs) {
+        // activations: wave wv fills rows 32*wv .. 32*wv+31 (4 x 64 slots of 16 bytes); slot p holds chunk
+        // (p % 8) ^ (row % 8) of row p / 8, and row % 8 == (lane / 8) % 8 for every slot of this lane
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int ch = tid + i * 256, tl = ch >> 3, kc = ch & 7;
-            const int t = t0 + tl;
-            areg[i] = t < M ? *reinterpret_cast<const uint4*>(xq + (size_t)t * K + (size_t)g * GROUP + kc * 16)
-                            : make_uint4(0, 0, 0, 0);
+            const int a_c = (lane & 7) ^ ((lane >> 3) & 7);
+            const uint32_t a_off = (uint32_t)min(t0 + wv * 32 + (lane >> 3) + 8 * i, M - 1) * (uint32_t)K + (uint32_t)a_c * 16;
+            lds_load16(xq + a_off + (uint32_t)g * GROUP, As + (wv * 256 + i * 64) * 16);   // rows past M: any valid row
         }
+        if (BITS == 8) {
 #pragma unroll
-        for (int c = 0; c < NC / 2; c++) breg[c] = bsrc[((size_t)g * NC + bh * (NC / 2) + c) * 64];
-        if (tid < PF_BM) mxreg = (mx && t0 + tid < M) ? (uint32_t)mx[(size_t)(t0 + tid) * G + g] : 1u;
+            for (int i = 0; i < 4; i++) {
+                const int p = wv * 256 + i * 64 + lane, r = p >> 3, c = (p & 7) ^ (r & 7);
+                const uint32_t b_off = (uint32_t)(((r >> 6) * G + g) * NC + c) * 1024u + (uint32_t)(r & 63) * 16;
+                lds_load16(wbase + b_off, Bs + (wv * 256 + i * 64) * 16);
+            }
+        } else {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int nl = wn * 64 + j * 32 + l32;
-            mreg[j] = ms[((size_t)(tile0 + (nl >> 6)) * G + g) * 64 + (nl & 63)];
+            for (int c = 0; c < NC / 2; c++) {
+                const int cc = (wv & 1) * (NC / 2) + c;
+                const uint32_t o = (uint32_t)(((wv >> 1) * G + g) * NC + cc) * 1024u;
+                lds_load16(wbase + o + lane * 16, Bp + ((wv >> 1) * NC + cc) * 1024);
+            }
+        }
+        sreg = s_ptr[(uint32_t)g * s_step];
+    };
+    // wait for this wave's copies, stage the multiplier, unpack W4/W6 codes into Bs
+    auto finish = [&](int8_t* Bs, uint32_t* sdst, bool real) {
+        __builtin_amdgcn_sched_barrier(0);       // keep the wait after the scaling arithmetic of compute()
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint32_t v = x_one ? 1u : sreg;
+        *sdst = v;
+        rsum += real ? (int)v - DIG_C : 0;
+        if (BITS != 8) {
+            // 64 codes = two 32-code blocks; each block's NC words sit in the wave's own staging planes
+            const int r = (wv >> 1) * 64 + lane, h = wv & 1;
+            const uint8_t* pl = Bp + ((wv >> 1) * NC + h * (NC / 2)) * 1024 + lane * 16;
+            uint32_t q[2 * NC];
+#pragma unroll
+            for (int c = 0; c < NC / 2; c++) {       // 16-byte chunk reads: a wave reads 1 KB contiguous
+                const uint4 v = *reinterpret_cast<const uint4*>(pl + c * 1024);
+                q[4 * c] = v.x; q[4 * c + 1] = v.y; q[4 * c + 2] = v.z; q[4 * c + 3] = v.w;
+            }
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                uint32_t o[8];
+                block_signed<BITS>(q + blk * NC, o);
+                *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2)) = make_uint4(o[0], o[1], o[2], o[3]);
+                *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2 + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
+            }
         }
     };
-    auto store = [&](int buf) {
+    // MFMA over one group from (As, Bs) and scaling into U
+    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss) {
+        // the constant first accumulator is rebuilt every group (16 moves) rather than held across the loop
+        v16i bias;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int ch = tid + i * 256, tl = ch >> 3, kc = ch & 7;
-            *reinterpret_cast<uint4*>(&As[buf][tl * PF_STR + kc * 16]) = areg[i];
-        }
-        uint32_t q[NC * 2];
-#pragma unroll
-        for (int c = 0; c < NC / 2; c++) { q[4 * c] = breg[c].x; q[4 * c + 1] = breg[c].y; q[4 * c + 2] = breg[c].z; q[4 * c + 3] = breg[c].w; }
-        uint32_t w[16];
-        block_signed<BITS>(q, w);
-        block_signed<BITS>(q + NC, w + 8);
-        uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][br * PF_STR + bh * 64]);
-#pragma unroll
-        for (int c = 0; c < 4; c++) dst[c] = make_uint4(w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]);
-        if (tid < PF_BM) mxs[buf][tid] = mxreg;
-    };
-
-    load(0);
-    store(0);
-    uint32_t mcur[2] = {mreg[0], mreg[1]};
-    __syncthreads();
-    for (int g = 0; g < G; g++) {
-        const int buf = g & 1;
-        if (g + 1 < G) load(g + 1);
+        for (int r = 0; r < 16; r++) asm volatile("v_mov_b32 %0, %1" : "=v"(bias[r]) : "i"(PF_BIAS));
         v16i d[2][2];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             v4i a[2], b[2];
 #pragma unroll
             for (int i = 0; i < 2; i++)
-                a[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm * 64 + i * 32 + l32) * PF_STR + s * 32 + lh * 16]);
+                a[i] = *reinterpret_cast<const v4i*>(As + swz(wm * 64 + i * 32 + l32, 2 * s + lh));
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                b[j] = *reinterpret_cast<const v4i*>(&Bs[buf][(wn * 64 + j * 32 + l32) * PF_STR + s * 32 + lh * 16]);
+                b[j] = *reinterpret_cast<const v4i*>(Bs + swz(wn * 64 + j * 32 + l32, 2 * s + lh));
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -387,11 +428,12 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                     d[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], s == 0 ? bias : d[i][j], 0, 0, 0);
         }
         // element (t, n) of a 32x32 tile: lane (n % 32) + 32 * ((t / 4) % 2), register 4 * (t / 8) + t % 4
+        const uint32_t mcur[2] = {mss[wn * 64 + l32], mss[wn * 64 + 32 + l32]};
 #pragma unroll
         for (int i = 0; i < 2; i++) {
 #pragma unroll
             for (int q4 = 0; q4 < 4; q4++) {
-                const uint4 mv = *reinterpret_cast<const uint4*>(&mxs[buf][wm * 64 + i * 32 + 8 * q4 + 4 * lh]);
+                const uint4 mv = *reinterpret_cast<const uint4*>(mxs + wm * 64 + i * 32 + 8 * q4 + 4 * lh);
                 const uint32_t mxv[4] = {mv.x, mv.y, mv.z, mv.w};
 #pragma unroll
                 for (int e = 0; e < 4; e++)
@@ -402,78 +444,126 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                     }
             }
         }
-        if (g + 1 < G) {
-            store(buf ^ 1);
-            mcur[0] = mreg[0];
-            mcur[1] = mreg[1];
-        }
+    };
+
+    // The copy of the next group is issued unconditionally (past the last group it re-reads group G-1 into the
+    // idle buffer), so each half-iteration is one basic block and the scheduling barriers hold.
+    issue(0, As0, Bs0);
+    finish(Bs0, s_dst0, true);
+    __syncthreads();
+    for (int g = 0; g < G; g += 2) {
+        issue(min(g + 1, G - 1), As1, Bs1);
+        compute(As0, Bs0, mxs0, mss0);
+        finish(Bs1, s_dst1, g + 1 < G);
+        __syncthreads();
+        if (g + 1 >= G) break;
+        issue(min(g + 2, G - 1), As0, Bs0);
+        compute(As1, Bs1, mxs1, mss1);
+        finish(Bs0, s_dst0, g + 2 < G);
         __syncthreads();
     }
 
-    // ---- bias correction: S = sum_g m * mx from balanced digits on the MFMA
-    __shared__ int Ra[PF_BM], Rb[PF_BN];
-    if (tid < PF_BM) {
-        const int t = t0 + tid;
-        int r = 0;
-        for (int g = 0; g < G; g++) r += (int)((mx && t < M) ? mx[(size_t)t * G + g] : 1u) - DIG_C;
-        Ra[tid] = r;
-    } else {
-        const int nl = tid - PF_BM;
-        int r = 0;
-        for (int g = 0; g < G; g++) r += (int)ms[((size_t)(tile0 + (nl >> 6)) * G + g) * 64 + (nl & 63)] - DIG_C;
-        Rb[nl] = r;
-    }
-    __syncthreads();
-    const long long GC2 = (long long)G * DIG_C * DIG_C;
+    // ---- bias correction and epilogue.  S = sum_g m * mx comes from balanced digits on the MFMA, 32 groups at a
+    // time: the multipliers of those groups are staged in the (now idle) LDS buffers, xs[t][32] = mx and
+    // ws[n][32] = m (uint16), and U -= B * (65536 D11 + 256 (D10 + D01) + D00) is applied per step (it is linear).
+    uint16_t* xs = reinterpret_cast<uint16_t*>(As0);            // PF_BM * 32 * 2 = 8 KB
+    uint16_t* ws = reinterpret_cast<uint16_t*>(Bs0);            // PF_BN * 32 * 2 = 8 KB
+    if (tid < PF_BM) Ra[tid] = rsum;
+    else Rb[tid - PF_BM] = rsum;
+    for (int k0 = 0; k0 < G; k0 += 32) {
+        __syncthreads();
+        for (int e = tid; e < PF_BM * 32; e += 256) {
+            const int rl = e >> 5, g = k0 + (e & 31);
+            // a multiplier of 32896 has zero digits: groups past G add nothing
+            xs[e] = g < G ? ((mx && t0 + rl < M) ? mx[(size_t)(t0 + rl) * G + g] : (uint16_t)1) : (uint16_t)DIG_C;
+            ws[e] = g < G ? ms[((size_t)(tile0 + (rl >> 6)) * G + g) * 64 + (rl & 63)] : (uint16_t)DIG_C;
+        }
+        __syncthreads();
+        v4i A1[2], A0[2], B1[2], B0[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int tl = wm * 64 + i * 32 + l32;            // A-operand row of this lane
-        const int ta = t0 + tl;
+        for (int i = 0; i < 2; i++) {
+            const int ta = wm * 64 + i * 32 + l32;       // A-operand row (token) of this lane
+            const int nb = wn * 64 + i * 32 + l32;       // B-operand column (row n) for the j = i tile
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int nl = wn * 64 + j * 32 + l32;        // B-operand column of this lane (and output column)
-            const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-            v16i d11 = z, d10 = z, d01 = z, d00 = z;
-            for (int k0 = 0; k0 < G; k0 += 32) {
-                int a1[16], a0[16], b1[16], b0[16];
+            for (int w = 0; w < 4; w++) {
+                uint32_t pa1 = 0, pa0 = 0, pb1 = 0, pb0 = 0;
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int g = k0 + lh * 16 + e;
-                    a1[e] = a0[e] = b1[e] = b0[e] = 0;
-                    if (g < G) {
-                        const uint32_t xv = (mx && ta < M) ? (uint32_t)mx[(size_t)ta * G + g] : 1u;
-                        digits16(xv, a1[e], a0[e]);
-                        const uint32_t mv = ms[((size_t)(tile0 + (nl >> 6)) * G + g) * 64 + (nl & 63)];
-                        digits16(mv, b1[e], b0[e]);
-                    }
+                for (int e = 0; e < 4; e++) {
+                    const int gl = lh * 16 + 4 * w + e;
+                    int a1, a0, b1, b0;
+                    digits16(xs[ta * 32 + gl], a1, a0);
+                    digits16(ws[nb * 32 + gl], b1, b0);
+                    pa1 |= (uint32_t)(a1 & 255) << (8 * e);
+                    pa0 |= (uint32_t)(a0 & 255) << (8 * e);
+                    pb1 |= (uint32_t)(b1 & 255) << (8 * e);
+                    pb0 |= (uint32_t)(b0 & 255) << (8 * e);
                 }
-                v4i A1, A0, B1, B0;
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    A1[w] = (a1[4 * w] & 255) | ((a1[4 * w + 1] & 255) << 8) | ((a1[4 * w + 2] & 255) << 16) | ((a1[4 * w + 3] & 255) << 24);
-                    A0[w] = (a0[4 * w] & 255) | ((a0[4 * w + 1] & 255) << 8) | ((a0[4 * w + 2] & 255) << 16) | ((a0[4 * w + 3] & 255) << 24);
-                    B1[w] = (b1[4 * w] & 255) | ((b1[4 * w + 1] & 255) << 8) | ((b1[4 * w + 2] & 255) << 16) | ((b1[4 * w + 3] & 255) << 24);
-                    B0[w] = (b0[4 * w] & 255) | ((b0[4 * w + 1] & 255) << 8) | ((b0[4 * w + 2] & 255) << 16) | ((b0[4 * w + 3] & 255) << 24);
-                }
-                d11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, d11, 0, 0, 0);
-                d10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, d10, 0, 0, 0);
-                d01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, d01, 0, 0, 0);
-                d00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, d00, 0, 0, 0);
+                A1[i][w] = (int)pa1; A0[i][w] = (int)pa0; B1[i][w] = (int)pb1; B0[i][w] = (int)pb0;
             }
-            const int n = n0 + nl;
-            const float cn = n < N ? cs[n] : 0.0f;
-            const long long rb = Rb[nl];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+                const v16i d11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1[i], B1[j], z, 0, 0, 0);
+                v16i d1x = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1[i], B0[j], z, 0, 0, 0);
+                d1x = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0[i], B1[j], d1x, 0, 0, 0);
+                const v16i d00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0[i], B0[j], z, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int t1 = (d11[r] << 8) + d1x[r];            // |t1| < 2^30
+                    const long long S = ((long long)t1 << 8) + d00[r];
+                    U[i][j][r] -= (unsigned long long)S << 21;
+                }
+            }
+    }
+    const long long GC2 = (long long)G * DIG_C * DIG_C;
+    float v[2][2][16];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int nb = wn * 64 + j * 32 + l32;
+        const int n = n0 + nb;
+        const float cn = n < N ? cs[n] : 0.0f;
+        const int rb = Rb[nb];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int tr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const long long S = 65536LL * d11[r] + 256LL * ((long long)d10[r] + d01[r]) + d00[r] +
-                                    (long long)DIG_C * ((long long)Ra[tr] + rb) + GC2;
-                const long long acc = (long long)(U[i][j][r] - ((unsigned long long)S << 21));
-                const int t = t0 + tr;
-                if (t < M && n < N) out.store(N, t, n, (i64_to_f(acc) * cn) * sx[t]);
+                const long long rest = (long long)DIG_C * (Ra[tr] + rb) + GC2;
+                const long long acc = (long long)(U[i][j][r] - ((unsigned long long)rest << 21));
+                v[i][j][r] = ((float)acc * cn) * sx[min(t0 + tr, M - 1)];   // int64 -> fp32 rounds to nearest even
             }
-        }
     }
+    // Accumulate loads every old value before the first store, so no store waits on a load
+    if (out.acc) {
+        float old[2][2][16];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int n = n0 + wn * 64 + j * 32 + l32, t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    old[i][j][r] = (t < M && n < N) ? *out.ptr(N, t, n) : 0.0f;
+                }
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) v[i][j][r] = old[i][j][r] + v[i][j][r];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int n = n0 + wn * 64 + j * 32 + l32, t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (t < M && n < N) *out.ptr(N, t, n) = v[i][j][r];
+            }
 }
 
 // ------------------------------------------------------------------ load-time repack and quantizer
@@ -622,8 +712,8 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
     } else if (M <= 64) {
         launch_mfma<BITS, 64>(L, xq, sx, mx, M, y, st);
     } else {
-        dim3 grid((L.N + PF_BN - 1) / PF_BN, (M + PF_BM - 1) / PF_BM);
-        k_prefill<BITS><<<grid, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y);
+        const int nbn = (L.N + PF_BN - 1) / PF_BN, nbt = (M + PF_BM - 1) / PF_BM;
+        k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
         DET_CHECK(hipGetLastError());
     }
 }
@@ -635,7 +725,8 @@ extern "C" {
 void det_linear_sizes(int N, int K, int bits, size_t* wq_bytes, size_t* c_bytes, size_t* m_bytes) {
     if (K <= 0 || K % GROUP || N <= 0) DET_FAIL("det_linear_sizes: bad shape N=%d K=%d", N, K);
     if (bits != 4 && bits != 6 && bits != 8) DET_FAIL("det_linear_sizes: unsupported bits=%d", bits);
-    const size_t T = ((size_t)N + TILE_N - 1) / TILE_N, G = (size_t)K / GROUP;
+    // whole 128-row blocks (pairs of 64-row tiles): the prefill kernel reads weight tiles two at a time
+    const size_t T = 2 * (((size_t)N + 2 * TILE_N - 1) / (2 * TILE_N)), G = (size_t)K / GROUP;
     if (wq_bytes) *wq_bytes = T * G * group_bytes(bits) * TILE_N;
     if (c_bytes) *c_bytes = T * TILE_N * 4;
     if (m_bytes) *m_bytes = T * G * TILE_N * 2;

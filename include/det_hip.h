@@ -30,11 +30,12 @@ void*       det_hip_stream(void);           // the stream det's work runs on (de
 // ---- weights: a quantized linear y = W x, W[N][K] (spec §2; det_cuda.h:27-32)
 // Same struct as det_cuda.h.  The pointers hold the HIP layout that det_linear_repack writes (the layout is
 // private to this backend, as the Metal backend's tiled codes are to it):
-//   wq: packed codes in 64-row tiles, [ceil(N/64)][K/128][GB/16][64 rows][16 bytes], where GB = 128, 96, 64 bytes
-//       is one row's packed 128-group (4 * bytes_per_32) for W8, W6, W4; the 16-byte chunk c of a tile row is bytes
-//       [16c, 16c+16) of that row's packed group, exactly as in the det row; rows past N are zero;
-//   c:  [ceil(N/64)*64] fp32 (zero past N);
-//   m:  [ceil(N/64)][K/128][64] uint16 (zero past N).
+//   wq: packed codes in 64-row tiles, [T][K/128][GB/16][64 rows][16 bytes] with T = 2*ceil(N/128) (whole pairs of
+//       tiles), where GB = 128, 96, 64 bytes is one row's packed 128-group (4 * bytes_per_32) for W8, W6, W4; the
+//       16-byte chunk c of a tile row is bytes [16c, 16c+16) of that row's packed group, exactly as in the det row;
+//       rows past N are zero;
+//   c:  [T*64] fp32 (zero past N);
+//   m:  [T][K/128][64] uint16 (zero past N).
 typedef struct {
     const uint8_t* wq;
     const float*   c;
@@ -72,9 +73,9 @@ void det_silu_mul_quant(const float* g, const float* u, int M, int n, float* h, 
 void det_gemm(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, hipStream_t st);
 void det_gemm_ex(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, int accumulate,
                  int nparts, const int* offs, float* const* dsts, hipStream_t st);
-// Scratch (det_cuda.h:52-57).  The HIP kernels keep their split-K partial sums in a buffer the library owns;
-// a caller-provided buffer of at least det_gemm_scratch_bytes(M, K) bytes is accepted for compatibility and
-// kept registered, and is never required.
+// Scratch (det_cuda.h:52-57).  The HIP kernels need no scratch (the W4/W6 activation-sum correction of the CUDA
+// tensor-core path does not exist here; split-K sums stay in LDS).  Both calls are kept for ABI compatibility:
+// det_gemm_scratch_bytes returns the reference's size, and a registered buffer is accepted and never touched.
 size_t det_gemm_scratch_bytes(int M, int K);
 void det_gemm_set_scratch(void* p, size_t bytes);
 

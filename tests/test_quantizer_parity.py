@@ -42,7 +42,7 @@ def test_repack_layout(bits):
     lin = ffi.Linear(rows, K, bits)
     wq, c, m = lin.wq.download(), lin.c.download(), lin.m.download()
     G, GB = K // 128, 4 * {8: 32, 6: 24, 4: 16}[bits]
-    T = (N + 63) // 64
+    T = 2 * ((N + 127) // 128)
     nc = K // 32 * {8: 32, 6: 24, 4: 16}[bits]
     planes = wq.reshape(T, G, GB // 16, 64, 16)
     for n in range(T * 64):
