@@ -18,6 +18,8 @@ HIPFLAGS = [
     '-fhip-fp32-correctly-rounded-divide-sqrt',
     # packed fp32 VALU ops are kept out of the generated code
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    # MFMA results in architectural VGPRs (the VALU scales them every 128-group; AGPRs would need copies)
+    '-mllvm', '-amdgpu-mfma-vgpr-form=1',
     '-Wall', '-Wno-unused-function',
 ]
 

@@ -83,6 +83,34 @@ template <> __device__ __forceinline__ void block_signed<6>(const uint32_t* q, u
     for (int j = 0; j < 8; j++) s[j] = (u[j] + ADD) ^ X;
 }
 
+// One 32-code block as unsigned codes u = wq + OFF (W4: 0..15, W6: 0..63), 8 words in k order.  These are valid
+// non-negative int8 operands; the -OFF part of the codes is applied separately (on the MFMA, as x . (-OFF)).
+template <int BITS> __device__ __forceinline__ void block_unsigned(const uint32_t* q, uint32_t* u);
+template <> __device__ __forceinline__ void block_unsigned<4>(const uint32_t* q, uint32_t* u) {
+    constexpr uint32_t LM = 0x0F0F0F0Fu;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        u[j] = q[j] & LM;
+        u[j + 4] = (q[j] >> 4) & LM;
+    }
+}
+template <> __device__ __forceinline__ void block_unsigned<6>(const uint32_t* q, uint32_t* u) {
+    constexpr uint32_t LM = 0x0F0F0F0Fu, HM = 0x30303030u;
+    const uint32_t h0 = q[4], h1 = q[5];
+    u[0] = (q[0] & LM) | ((h0 << 4) & HM);
+    u[1] = (q[1] & LM) | ((h1 << 4) & HM);
+    u[2] = (q[2] & LM) | ((h0 << 2) & HM);
+    u[3] = (q[3] & LM) | ((h1 << 2) & HM);
+    u[4] = ((q[0] >> 4) & LM) | (h0 & HM);
+    u[5] = ((q[1] >> 4) & LM) | (h1 & HM);
+    u[6] = ((q[2] >> 4) & LM) | ((h0 >> 2) & HM);
+    u[7] = ((q[3] >> 4) & LM) | ((h1 >> 2) & HM);
+}
+template <> __device__ __forceinline__ void block_unsigned<8>(const uint32_t* q, uint32_t* u) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) u[j] = q[j];
+}
+
 // int64 += int32 * uint32 (one 32x32->64 unsigned multiply-add and a sign fix of the high word)
 __device__ __forceinline__ void mac_s32_u32(long long& acc, int p, uint32_t s) {
     unsigned long long r = (unsigned long long)(uint32_t)p * (unsigned long long)s + (unsigned long long)acc;
@@ -304,7 +332,8 @@ template <int BITS>
 __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                       const uint16_t* __restrict__ ms, int N, int K,
                                                       const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                      const uint16_t* __restrict__ mx, int M, Out out, int nbn, int nbt) {
+                                                      const uint16_t* __restrict__ mx, const int* __restrict__ cinit, int M,
+                                                      Out out, int nbn, int nbt) {
     constexpr int NC = group_bytes(BITS) / 16;
     constexpr int PK = BITS == 8 ? 16 : 2 * NC * 1024;         // packed staging bytes (W4/W6)
     // Two buffers as distinct LDS objects, selected at compile time (the loop is unrolled by two), so that the
@@ -313,11 +342,13 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     __shared__ __attribute__((aligned(16))) int8_t As0[PF_BM * 128], As1[PF_BM * 128];
     __shared__ __attribute__((aligned(16))) int8_t Bs0[PF_BN * 128], Bs1[PF_BN * 128];
     __shared__ __attribute__((aligned(16))) uint8_t Bp[PK];
-    __shared__ __attribute__((aligned(16))) uint32_t mxs0[PF_BM], mxs1[PF_BM];   // mx[t][g] of the buffer's group
-    __shared__ __attribute__((aligned(16))) uint32_t mss0[PF_BN], mss1[PF_BN];   // m[n][g]
-    __shared__ int Ra[PF_BM], Rb[PF_BN];
+    // multipliers of the buffer's group: [0, 128) mx[t][g] of the tile's tokens, [128, 256) m[n][g] of its rows
+    __shared__ __attribute__((aligned(16))) uint32_t mul0[PF_BM + PF_BN], mul1[PF_BM + PF_BN];
+    __shared__ __attribute__((aligned(16))) int cis0[PF_BM], cis1[PF_BM];        // first accumulator per token (W4/W6)
+    __shared__ __attribute__((aligned(16))) int pf_sink[64];           // target of the L2 prefetch copies (never read)
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);        // the wave index as a scalar
     const int wm = wv >> 1, wn = wv & 1;
     // XCD-aware tile order: consecutive workgroup ids go to different XCDs; give each XCD a contiguous run of
     // tiles (row-block major) so that the token blocks sharing one weight tile run on the same L2.
@@ -341,50 +372,87 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     // W4/W6 into the Bp planes (wave wv: tile wv >> 1, chunk planes (wv & 1) * NC/2 .. +NC/2, which are exactly
     // the half-groups this wave unpacks itself).  Per-lane addresses are 32-bit offsets from uniform bases.
     const uint8_t* wbase = wq + (size_t)tile0 * G * NC * 1024;
-    // per-group multipliers: thread tid < 128 stages mx of token t0 + tid, the others m of row n0 + tid - 128
-    // (branch-free: a thread whose multiplier is implicitly 1 reads a valid m entry and discards it)
-    const bool x_one = tid < PF_BM && !(mx && t0 + tid < M);
-    const uint16_t* s_ptr = (tid < PF_BM && !x_one) ? mx + (size_t)(t0 + tid) * G
-                                                    : ms + (size_t)((tile0 + ((tid & 127) >> 6)) * G) * 64 + (tid & 63);
-    const uint32_t s_step = (tid < PF_BM && !x_one) ? 1u : 64u;
-    uint32_t* const s_dst0 = tid < PF_BM ? mxs0 + tid : mss0 + (tid - PF_BM);
-    uint32_t* const s_dst1 = tid < PF_BM ? mxs1 + tid : mss1 + (tid - PF_BM);
+    // per-group multipliers: thread tid < 128 (waves 0, 1) stages mx of token t0 + tid, the others (waves 2, 3) m of
+    // row n0 + tid - 128, through buffer loads (the resource is uniform per wave); a missing mx (NULL) or a token
+    // past M reads as zero and stages 1.  W4/W6 also stage the token's first accumulator cinit[t][g].
+    const bool xw = wvu < 2;
+    const __amdgpu_buffer_rsrc_t sr = xw ? __builtin_amdgcn_make_buffer_rsrc((void*)mx, (short)0, mx ? M * G * 2 : 0, 0x00020000)
+                                         : __builtin_amdgcn_make_buffer_rsrc((void*)ms, (short)0, (tile0 + 2) * G * 128, 0x00020000);
+    const uint32_t s_vo = xw ? (uint32_t)(t0 + tid) * (uint32_t)G * 2
+                             : (uint32_t)((tile0 + ((tid - PF_BM) >> 6)) * G * 64 + ((tid - PF_BM) & 63)) * 2;
+    const int s_step = xw ? 2 : 128;
+    const bool x_one = xw && !(mx && t0 + tid < M);
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc((void*)cinit, (short)0, cinit ? M * G * 4 : 0, 0x00020000);
+    const uint32_t c_vo = (uint32_t)(t0 + (tid & 127)) * (uint32_t)G * 4;     // rows past M: out of range, zero
     uint32_t sreg = 1;
     int rsum = 0;          // Ra (tid < 128) or Rb (tid >= 128): sum over groups of (multiplier - 32896)
 
-    // copy group g into (As, Bs / Bp) and its multiplier into sreg; nothing waits here
-    auto issue = [&](int g, int8_t* As, int8_t* Bs) {
-        // activations: wave wv fills rows 32*wv .. 32*wv+31 (4 x 64 slots of 16 bytes); slot p holds chunk
-        // (p % 8) ^ (row % 8) of row p / 8, and row % 8 == (lane / 8) % 8 for every slot of this lane
+    // Global -> LDS copies use buffer resources: one 32-bit per-lane offset, the rest in scalar offsets, and the
+    // hardware range check returns zeros for token rows past M.
+    // one resource per 8-row step i (base row + 8 i), so the per-lane offset is a single register and rows past M
+    // fall outside the resource's range
+    __amdgpu_buffer_rsrc_t xr[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int a_c = (lane & 7) ^ ((lane >> 3) & 7);
-            const uint32_t a_off = (uint32_t)min(t0 + wv * 32 + (lane >> 3) + 8 * i, M - 1) * (uint32_t)K + (uint32_t)a_c * 16;
-            lds_load16(xq + a_off + (uint32_t)g * GROUP, As + (wv * 256 + i * 64) * 16);   // rows past M: any valid row
-        }
+    for (int i = 0; i < 4; i++)
+        xr[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(xq + (size_t)i * 8 * K), (short)0, max(0, (M - 8 * i) * K), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, 2 * G * NC * 1024, 0x00020000);
+    // activations: wave wv fills rows 32*wv .. 32*wv+31 (4 x 64 slots of 16 bytes); slot p holds chunk
+    // (p % 8) ^ (row % 8) of row p / 8, and row % 8 == (lane / 8) % 8 for every slot of this lane
+    const uint32_t a_vo = (uint32_t)(t0 + wv * 32 + (lane >> 3)) * (uint32_t)K + (uint32_t)(((lane & 7) ^ ((lane >> 3) & 7)) * 16);
+    // W8 codes: slot p = row r * 8 + position q takes chunk q ^ (r & 7) of row r, r = 32 * (wv & 1) + 8 i + lane / 8
+    // within tile wv >> 1
+    const uint32_t b_vo = BITS == 8 ? (uint32_t)(((lane & 7) ^ ((lane >> 3) & 7)) * 1024 + (lane >> 3) * 16) : (uint32_t)lane * 16;
+
+    // L2 prefetch offsets: waves 0-1 cover the 2 * NC * 8 lines (128 bytes) of the tile pair's group (line L of
+    // tile L / (8 NC)), waves 2-3 one line of each of the 128 token rows
+    uint32_t pf_vo;
+    if (xw) {
+        const int L = wv * 64 + lane, lt = L / (NC * 8), lw = L - lt * (NC * 8);
+        pf_vo = lt < 2 ? (uint32_t)((lt * G * NC) * 1024 + lw * 128) : 0u;
+    } else {
+        pf_vo = (uint32_t)(t0 + (wv - 2) * 64 + lane) * (uint32_t)K;     // rows past M: out of range
+    }
+    // copy group g into (As, Bs / Bp) and its multiplier into sreg; nothing waits here
+    auto issue = [&](int g, int8_t* As, int8_t* Bs, int* cis) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr[i], (__attribute__((address_space(3))) void*)(As + (wvu * 256 + i * 64) * 16), 16,
+                                                     a_vo, g * GROUP, 0, 0);
         if (BITS == 8) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = wv * 256 + i * 64 + lane, r = p >> 3, c = (p & 7) ^ (r & 7);
-                const uint32_t b_off = (uint32_t)(((r >> 6) * G + g) * NC + c) * 1024u + (uint32_t)(r & 63) * 16;
-                lds_load16(wbase + b_off, Bs + (wv * 256 + i * 64) * 16);
-            }
+            for (int i = 0; i < 4; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(Bs + (wvu * 256 + i * 64) * 16), 16,
+                                                         b_vo, (((wvu >> 1) * G + g) * NC) * 1024 + ((wvu & 1) * 32 + i * 8) * 16, 0, 0);
         } else {
 #pragma unroll
             for (int c = 0; c < NC / 2; c++) {
-                const int cc = (wv & 1) * (NC / 2) + c;
-                const uint32_t o = (uint32_t)(((wv >> 1) * G + g) * NC + cc) * 1024u;
-                lds_load16(wbase + o + lane * 16, Bp + ((wv >> 1) * NC + cc) * 1024);
+                const int cc = (wvu & 1) * (NC / 2) + c;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(Bp + ((wvu >> 1) * NC + cc) * 1024), 16,
+                                                         b_vo, (((wvu >> 1) * G + g) * NC + cc) * 1024, 0, 0);
             }
         }
-        sreg = s_ptr[(uint32_t)g * s_step];
+        sreg = __builtin_amdgcn_raw_buffer_load_b16(sr, s_vo, g * s_step, 0);
+        if (BITS != 8 && xw)   // W4/W6 first accumulators straight into LDS (waves 0 and 1: 64 tokens each)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(cr, (__attribute__((address_space(3))) void*)(cis + wvu * 64), 4, c_vo, g * 4, 0, 0);
+        // L2 prefetch of group g + 1 (the group after the one copied here): one dword per 128-byte line, waves 0-1
+        // the weight tiles, waves 2-3 the activation rows.  It is the last memory op of the wave, so the group's own
+        // copies are complete at vmcnt(1).
+        {
+            const int gp = min(g + 1, G - 1);
+            if (xw)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)pf_sink, 4,
+                                                         pf_vo, gp * NC * 1024, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr[0], (__attribute__((address_space(3))) void*)pf_sink, 4,
+                                                         pf_vo, gp * GROUP, 0, 0);
+        }
     };
     // wait for this wave's copies, stage the multiplier, unpack W4/W6 codes into Bs
     auto finish = [&](int8_t* Bs, uint32_t* sdst, bool real) {
         __builtin_amdgcn_sched_barrier(0);       // keep the wait after the scaling arithmetic of compute()
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");   // everything but the trailing L2 prefetch
         const uint32_t v = x_one ? 1u : sreg;
-        *sdst = v;
+        sdst[tid] = v;
         rsum += real ? (int)v - DIG_C : 0;
         if (BITS != 8) {
             // 64 codes = two 32-code blocks; each block's NC words sit in the wave's own staging planes
@@ -399,38 +467,51 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
 #pragma unroll
             for (int blk = 0; blk < 2; blk++) {
                 uint32_t o[8];
-                block_signed<BITS>(q + blk * NC, o);
+                block_unsigned<BITS>(q + blk * NC, o);
                 *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2)) = make_uint4(o[0], o[1], o[2], o[3]);
                 *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2 + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
             }
         }
     };
     // MFMA over one group from (As, Bs) and scaling into U
-    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss) {
-        // the constant first accumulator is rebuilt every group (16 moves) rather than held across the loop
-        v16i bias;
+    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss, const int* cis) {
+        // W4/W6 tiles hold u = wq + OFF; their chains start from B - OFF * sum(x) of the token (staged per group in
+        // cis), so that d = B + x . u - OFF * sum(x) = B + x . wq.  W8 chains start from B.  The start values of
+        // token tile i are read right before its first two MFMAs, so only 16 of them are live at a time.
+        auto cinit_of = [&](int i) {
+            v16i c;
+            if (BITS != 8) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) asm volatile("v_mov_b32 %0, %1" : "=v"(bias[r]) : "i"(PF_BIAS));
-        v16i d[2][2];
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const int4 cv = *reinterpret_cast<const int4*>(cis + wm * 64 + i * 32 + 8 * q4 + 4 * lh);
+                    c[4 * q4] = cv.x; c[4 * q4 + 1] = cv.y; c[4 * q4 + 2] = cv.z; c[4 * q4 + 3] = cv.w;
+                }
+            } else {
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            v4i a[2], b[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-                a[i] = *reinterpret_cast<const v4i*>(As + swz(wm * 64 + i * 32 + l32, 2 * s + lh));
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                b[j] = *reinterpret_cast<const v4i*>(Bs + swz(wn * 64 + j * 32 + l32, 2 * s + lh));
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    d[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], s == 0 ? bias : d[i][j], 0, 0, 0);
-        }
-        // element (t, n) of a 32x32 tile: lane (n % 32) + 32 * ((t / 4) % 2), register 4 * (t / 8) + t % 4
+                for (int r = 0; r < 16; r++) asm volatile("v_mov_b32 %0, %1" : "=v"(c[r]) : "i"(PF_BIAS));
+            }
+            return c;
+        };
+        // one token tile at a time: its two n-tiles' MFMA chains (32 accumulator registers), then their scaling
         const uint32_t mcur[2] = {mss[wn * 64 + l32], mss[wn * 64 + 32 + l32]};
 #pragma unroll
         for (int i = 0; i < 2; i++) {
+            v16i d[2];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const v4i b0 = *reinterpret_cast<const v4i*>(Bs + swz(wn * 64 + l32, 2 * s + lh));
+                const v4i b1 = *reinterpret_cast<const v4i*>(Bs + swz(wn * 64 + 32 + l32, 2 * s + lh));
+                const v4i a = *reinterpret_cast<const v4i*>(As + swz(wm * 64 + i * 32 + l32, 2 * s + lh));
+                if (s == 0) {
+                    const v16i c = cinit_of(i);
+                    d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, c, 0, 0, 0);
+                    d[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, c, 0, 0, 0);
+                } else {
+                    d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, d[0], 0, 0, 0);
+                    d[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, d[1], 0, 0, 0);
+                }
+            }
+            // element (t, n) of a 32x32 tile: lane (n % 32) + 32 * ((t / 4) % 2), register 4 * (t / 8) + t % 4
 #pragma unroll
             for (int q4 = 0; q4 < 4; q4++) {
                 const uint4 mv = *reinterpret_cast<const uint4*>(mxs + wm * 64 + i * 32 + 8 * q4 + 4 * lh);
@@ -440,7 +521,7 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
                         const uint32_t sc = __umul24(mcur[j], mxv[e]);
-                        U[i][j][4 * q4 + e] += (unsigned long long)(uint32_t)d[i][j][4 * q4 + e] * sc;
+                        U[i][j][4 * q4 + e] += (unsigned long long)(uint32_t)d[j][4 * q4 + e] * sc;
                     }
             }
         }
@@ -448,26 +529,29 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
 
     // The copy of the next group is issued unconditionally (past the last group it re-reads group G-1 into the
     // idle buffer), so each half-iteration is one basic block and the scheduling barriers hold.
-    issue(0, As0, Bs0);
-    finish(Bs0, s_dst0, true);
+    issue(0, As0, Bs0, cis0);
+    finish(Bs0, mul0, true);
     __syncthreads();
     for (int g = 0; g < G; g += 2) {
-        issue(min(g + 1, G - 1), As1, Bs1);
-        compute(As0, Bs0, mxs0, mss0);
-        finish(Bs1, s_dst1, g + 1 < G);
+        issue(min(g + 1, G - 1), As1, Bs1, cis1);
+        compute(As0, Bs0, mul0, mul0 + PF_BM, cis0);
+        finish(Bs1, mul1, g + 1 < G);
         __syncthreads();
         if (g + 1 >= G) break;
-        issue(min(g + 2, G - 1), As0, Bs0);
-        compute(As1, Bs1, mxs1, mss1);
-        finish(Bs0, s_dst0, g + 2 < G);
+        issue(min(g + 2, G - 1), As0, Bs0, cis0);
+        compute(As1, Bs1, mul1, mul1 + PF_BM, cis1);
+        finish(Bs0, mul0, g + 2 < G);
         __syncthreads();
     }
 
     // ---- bias correction and epilogue.  S = sum_g m * mx comes from balanced digits on the MFMA, 32 groups at a
     // time: the multipliers of those groups are staged in the (now idle) LDS buffers, xs[t][32] = mx and
     // ws[n][32] = m (uint16), and U -= B * (65536 D11 + 256 (D10 + D01) + D00) is applied per step (it is linear).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");          // the last L2 prefetch copy has landed
     uint16_t* xs = reinterpret_cast<uint16_t*>(As0);            // PF_BM * 32 * 2 = 8 KB
     uint16_t* ws = reinterpret_cast<uint16_t*>(Bs0);            // PF_BN * 32 * 2 = 8 KB
+    int* Ra = reinterpret_cast<int*>(As1);                      // sums of (mx - 32896) per token
+    int* Rb = Ra + PF_BM;                                       // sums of (m - 32896) per row
     if (tid < PF_BM) Ra[tid] = rsum;
     else Rb[tid - PF_BM] = rsum;
     for (int k0 = 0; k0 < G; k0 += 32) {
@@ -519,7 +603,8 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
             }
     }
     const long long GC2 = (long long)G * DIG_C * DIG_C;
-    float v[2][2][16];
+    // epilogue, 16 outputs at a time; Accumulate loads all 16 old values before the first store, so no store waits
+    // on a load
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int nb = wn * 64 + j * 32 + l32;
@@ -527,43 +612,50 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         const float cn = n < N ? cs[n] : 0.0f;
         const int rb = Rb[nb];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < 2; i++) {
+            float v[16];
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int tr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 const long long rest = (long long)DIG_C * (Ra[tr] + rb) + GC2;
                 const long long acc = (long long)(U[i][j][r] - ((unsigned long long)rest << 21));
-                v[i][j][r] = ((float)acc * cn) * sx[min(t0 + tr, M - 1)];   // int64 -> fp32 rounds to nearest even
+                v[r] = ((float)acc * cn) * sx[min(t0 + tr, M - 1)];   // int64 -> fp32 rounds to nearest even
             }
-    }
-    // Accumulate loads every old value before the first store, so no store waits on a load
-    if (out.acc) {
-        float old[2][2][16];
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int i = 0; i < 2; i++)
+            if (out.acc) {
+                float old[16];
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int n = n0 + wn * 64 + j * 32 + l32, t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    old[i][j][r] = (t < M && n < N) ? *out.ptr(N, t, n) : 0.0f;
+                    const int t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    old[r] = (t < M && n < N) ? *out.ptr(N, t, n) : 0.0f;
                 }
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) v[i][j][r] = old[i][j][r] + v[i][j][r];
-    }
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int i = 0; i < 2; i++)
+                for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int n = n0 + wn * 64 + j * 32 + l32, t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (t < M && n < N) *out.ptr(N, t, n) = v[i][j][r];
+                const int t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (t < M && n < N) *out.ptr(N, t, n) = v[r];
             }
+        }
+    }
+}
+
+// First MFMA accumulator of each (token, group) for W4/W6: cinit[t][g] = 2^21 - OFF * sum_{k in g} xq[t][k]
+// (the prefill kernel multiplies unsigned codes u = wq + OFF; this restores x . wq and adds the bias B)
+__global__ void k_cinit(const int8_t* __restrict__ xq, int MG, int off, int* __restrict__ cinit) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;     // (t * G + g), and xq + idx * 128 is its group
+    if (idx >= MG) return;
+    const int4* p = reinterpret_cast<const int4*>(xq + (size_t)idx * GROUP);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int4 v = p[i];
+        s = __builtin_amdgcn_sdot4(v.x, 0x01010101, s, false);
+        s = __builtin_amdgcn_sdot4(v.y, 0x01010101, s, false);
+        s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
+        s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
+    }
+    cinit[idx] = (int)PF_BIAS - off * s;
 }
 
 // ------------------------------------------------------------------ load-time repack and quantizer
@@ -680,8 +772,32 @@ __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ w, i
 int g_num_cus = 0;
 int g_decode_waves = 2048;      // target waves per decode launch (split-K below it)
 int g_decode_max_m = 8;
-void* g_user_scratch = nullptr;     // registered for ABI compatibility; no HIP kernel needs it
+// Per-(token, group) first accumulators of the W4/W6 prefill path, M * (K/128) int32: normally the buffer registered
+// with det_gemm_set_scratch; without one (or with a too small one) a lazily grown global buffer, as in the reference
+// (gemm.cu:913-936): a one-time note on stderr, and only safe when all det_gemm calls are ordered on one stream.
+void* g_user_scratch = nullptr;
 size_t g_user_scratch_bytes = 0;
+int* g_cinit = nullptr;
+size_t g_cinit_cap = 0;             // elements
+
+int* cinit_scratch(int M, int G, hipStream_t st) {
+    const size_t need = (size_t)M * G;
+    if (g_user_scratch && need * sizeof(int) <= g_user_scratch_bytes) return (int*)g_user_scratch;
+    static bool noted = false;
+    if (!noted) {
+        fprintf(stderr, "det_gemm: note: no scratch (or too small, have %zu bytes, need %zu for M=%d K=%d) set with "
+                        "det_gemm_set_scratch; using a lazily allocated global buffer\n",
+                g_user_scratch_bytes, need * sizeof(int), M, G * GROUP);
+        noted = true;
+    }
+    if (need > g_cinit_cap) {
+        DET_CHECK(hipStreamSynchronize(st));     // earlier launches may still use the old buffer
+        if (g_cinit) DET_CHECK(hipFree(g_cinit));
+        g_cinit_cap = std::max(need, (size_t)4096 * 136);
+        DET_CHECK(hipMalloc(&g_cinit, g_cinit_cap * sizeof(int)));
+    }
+    return g_cinit;
+}
 
 template <int BITS, int MP>
 void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
@@ -713,7 +829,14 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         launch_mfma<BITS, 64>(L, xq, sx, mx, M, y, st);
     } else {
         const int nbn = (L.N + PF_BN - 1) / PF_BN, nbt = (M + PF_BM - 1) / PF_BM;
-        k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
+        int* ci = nullptr;
+        if (BITS != 8) {
+            const int G = L.K / GROUP;
+            ci = cinit_scratch(M, G, st);
+            k_cinit<<<(M * G + 255) / 256, 256, 0, st>>>(xq, M * G, BITS == 6 ? 32 : 8, ci);
+            DET_CHECK(hipGetLastError());
+        }
+        k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, ci, M, y, nbn, nbt);
         DET_CHECK(hipGetLastError());
     }
 }
