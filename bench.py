@@ -122,6 +122,19 @@ def shape_line(name, N, K, M, bits, ms):
             'frac_of_bound': round((gbs / HBM_PEAK_GBS) if bound == 'hbm' else (tops / INT8_PEAK_TOPS), 4)}
 
 
+def committed_traffic(kernel, grid):
+    """HBM bytes per launch of `kernel` at `grid` from the committed FETCH_SIZE/WRITE_SIZE summary (scaled by the
+    copy calibration), or None when the summary has no such row."""
+    path = os.path.join(ROOT, 'profiles', 'gemm_hbm_traffic.md')
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cols = [c.strip().strip('`') for c in line.split('|')]
+        if len(cols) > 6 and cols[1] == kernel and cols[2] == str(grid):
+            return int(cols[6])
+    return None
+
+
 def cpu_baseline(target_s=12.0):
     """Times the oracle's C GEMM (OpenMP over output rows) on a bounded row sample of the W6 M=512 workload."""
     threads = min(os.cpu_count() or 1, 16)
@@ -156,7 +169,17 @@ def main():
     ap.add_argument('--warmup', type=int, default=20)
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--only-main', action='store_true')
+    ap.add_argument('--copy-calibration', action='store_true',
+                    help='only run a plain device-to-device copy of 1 GiB, 10 times (scales FETCH_SIZE/WRITE_SIZE)')
     args = ap.parse_args()
+    if args.copy_calibration:
+        L = ffi.lib()
+        a, b = ffi.Buf(1 << 30, np.uint8), ffi.Buf(1 << 30, np.uint8)
+        for _ in range(10):
+            L.det_memcpy(b.ptr, a.ptr, 1 << 30, None)
+        L.det_sync()
+        print(json.dumps({'copy_bytes_per_launch': 1 << 30, 'launches': 10}))
+        return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py: this build measures one GPU only (the path shards along N with an all-gather of y; '
               'no multi-GPU figure is produced)', file=sys.stderr)
@@ -198,8 +221,11 @@ def main():
         'config': {'workload': 'BASELINE configs[1]: W6 prefill GEMM K=2560 N=9728 M=512 (det_gemm_ex Write)',
                    'M': 512, 'N': N6, 'K': K, 'bits': 6, 'device': device},
         'roofline': {'bound': 'mfma', 'achieved': tops, 'peak': INT8_PEAK_TOPS, 'unit': 'TFLOP/s',
-                     'frac': round(tops / INT8_PEAK_TOPS, 4), 'traffic': None,
-                     'kernel': 'k_mfma<6,128>', 'algorithmic_ops_per_launch': 2 * 512 * N6 * K},
+                     'frac': round(tops / INT8_PEAK_TOPS, 4),
+                     'traffic': committed_traffic('k_prefill<6>', ((N6 + 127) // 128) * 4 * 256),
+                     'traffic_source': 'profiles/gemm_hbm_traffic.md (FETCH_SIZE x2 + WRITE_SIZE x1 per launch)',
+                     'algorithmic_bytes_per_launch': algo_bytes(N6, K, 512, 6),
+                     'kernel': 'k_prefill<6> (+ k_cinit)', 'algorithmic_ops_per_launch': 2 * 512 * N6 * K},
         'shapes': shapes,
         'timed_wall_s': round(wall, 4),
     }

@@ -257,3 +257,51 @@ def test_golden_fixtures():
         if key.startswith('quantize_') and key.endswith('_rows'):
             bits = int(key.split('_')[2][1:])
             assert (oracle.quantize_rows(z[key[:-5] + '_w'], bits) == z[key]).all(), key
+
+
+# ---------------------------------------------------------------- fp32 primitives of the fused producers
+def ulp_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    return np.abs(got - want) / np.maximum(ulp, np.finfo(np.float32).smallest_subnormal)
+
+
+def test_transcendentals_against_math():
+    """exp_f / log_f / sigmoid_f / silu_f / softplus_f (spec/prim.rs:78-149) stay within a few ulp of the exact
+    functions (a wrong constant, sign or step would not), hit their closed forms, and follow their clamps."""
+    L = oracle.lib()
+    xs = np.linspace(-86.0, 88.0, 20001).astype(np.float32)
+    e = np.array([L.ora_exp_f(float(v)) for v in xs], np.float32)
+    assert ulp_err(e, np.exp(xs.astype(np.float64))).max() <= 2.0
+    assert L.ora_exp_f(0.0) == 1.0 and L.ora_exp_f(-87.5) == 0.0
+    assert L.ora_exp_f(1000.0) == L.ora_exp_f(88.0)                     # clamped at 88
+    ps = np.exp(np.linspace(-80, 80, 20001)).astype(np.float32)
+    lg = np.array([L.ora_log_f(float(v)) for v in ps], np.float32)
+    err = np.abs(lg.astype(np.float64) - np.log(ps.astype(np.float64)))
+    assert (err <= 4 * np.spacing(np.maximum(np.abs(np.log(ps)), 1e-3).astype(np.float32))).all()
+    assert L.ora_log_f(1.0) == 0.0
+    zs = np.linspace(-30, 30, 6001).astype(np.float32)
+    sg = np.array([L.ora_sigmoid_f(float(v)) for v in zs], np.float32)
+    assert ulp_err(sg, 1.0 / (1.0 + np.exp(-zs.astype(np.float64)))).max() <= 4.0
+    si = np.array([L.ora_silu_f(float(v)) for v in zs], np.float32)
+    assert ulp_err(si, zs.astype(np.float64) / (1.0 + np.exp(-zs.astype(np.float64)))).max() <= 6.0
+    sp = np.array([L.ora_softplus_f(float(v)) for v in zs], np.float32)
+    # log_f(1 + exp_f(x)) for -15 <= x <= 20 rounds 1 + e^x first: a few ulp of (1 + e^x) absolute
+    true_sp = np.log1p(np.exp(zs.astype(np.float64)))
+    bound = 4 * np.spacing((1.0 + np.exp(zs.astype(np.float64))).astype(np.float32)).astype(np.float64)
+    assert (np.abs(sp.astype(np.float64) - true_sp) <= np.maximum(bound, 6 * np.spacing(true_sp.astype(np.float32)))).all()
+    low = np.linspace(-40, -15.01, 500).astype(np.float32)                # x < -15: exp_f(x) itself
+    assert all(L.ora_softplus_f(float(v)) == L.ora_exp_f(float(v)) for v in low)
+    assert L.ora_softplus_f(25.0) == 25.0                                 # x > 20 returns x
+
+
+def test_treesum_order():
+    """treesum is the balanced pairwise tree over the row padded to a power of two (spec/prim.rs:154-170)."""
+    L = oracle.lib()
+    v = np.array([1e8, 1.0, 1.0, 1.0, -1e8, 3.0], np.float32)   # padded to 8: ((1e8+1)+(1+1)) + ((-1e8+3)+(0+0))
+    f = np.float32
+    want = (f(f(1e8) + f(1)) + f(f(1) + f(1))) + (f(f(-1e8) + f(3)) + f(0))
+    assert np.float32(L.ora_treesum(v.ctypes.data, v.size)) == want
+    ints = np.arange(1, 1001, dtype=np.float32)                   # exact integer sums are order-free
+    assert L.ora_treesum(ints.ctypes.data, ints.size) == 500500.0
