@@ -9,12 +9,12 @@
 // GB/16 chunk planes of [64 rows][16 bytes], so one wave instruction loads 1 KB of contiguous bytes.
 //
 // Kernels (chosen by shape only, like the reference's gemm_bits, gemm.cu:1016-1023):
-//   k_decode<BITS,MP> (M <= 8): one workgroup per 64-row tile, lane = output row.  The lane streams its row's
-//       packed groups with dwordx4 loads, unpacks to signed int8 words in registers, and dots them with the
-//       activations (uniform across the wave, so they are scalar loads) with v_dot4c_i32_i8; the int32 group partial
-//       is scaled by m*mx into int64.  When the tiles alone would not fill the chip, the groups are split over up
-//       to 16 waves of the workgroup and the int64 partial sums are added in LDS.
-//   k_mfma<BITS,BM> (M > 8): 128-row x BM-token workgroup tile, 4 waves of (BM/2) x 64.  Per 128-group the
+//   k_decode<BITS,MP> (M <= 16): 64-row tiles x K-slices, lane = output row.  Each wave streams one packed
+//       128-group at a time with dwordx4 loads (all issued before any arithmetic) and unpacks them to signed int8 words in
+//       registers.  M == 1: dots with the activations (scalar loads) by v_dot4c_i32_i8; 2 <= M <= 16: one
+//       v_mfma_i32_32x32x32_i8 per 16 k-bytes carries the 64 rows x MP tokens.  The int32 group partial is scaled by
+//       m*mx into int64; the waves of a workgroup add in LDS, the K-slices of a tile by int64 atomics.
+//   k_mfma<BITS,BM> (16 < M <= 64): 128-row x BM-token workgroup tile, 4 waves of (BM/2) x 64.  Per 128-group the
 //       activation tile and the unpacked (signed int8) weight tile are staged in LDS; v_mfma_i32_32x32x32_i8 gives
 //       the exact int32 group partials, which are scaled into int64 accumulators before the next group.
 #include <string.h>
@@ -118,73 +118,194 @@ __device__ __forceinline__ void mac_s32_u32(long long& acc, int p, uint32_t s) {
     acc = (long long)r;
 }
 
-// ------------------------------------------------------------------ decode (M <= 8)
-// One workgroup per 64-row tile with S waves; wave w takes the groups g = w, w + S, ...  The waves' exact int64
-// partial sums meet in LDS; wave w finishes tokens w, w + S, ...
+// ------------------------------------------------------------------ decode (M <= 16)
+// Grid: T tiles x KS K-slices, one workgroup each, S waves per workgroup; wave w of slice k takes the groups
+// g0(k) + w, g0(k) + w + S, ... (normally exactly one), issuing all its loads before any arithmetic.  The waves'
+// exact int64 sums meet in LDS.  With KS > 1 every slice adds its sums into part[t][n] with int64 atomics, waits
+// until they are performed, then counts itself in cnt[tile]; the workgroup that arrives last takes the totals by
+// atomic exchange with 0, runs the epilogue and resets the counter, so part and cnt are zero again between calls.
+// No workgroup waits for another.  Atomics are coherent across the XCDs' L2s, so no cache write-back is needed.
 constexpr int DEC_MAXW = 16;
+#ifndef DEC_GPW_
+#define DEC_GPW_ 1
+#endif
+#ifndef DEC_MMA_MIN
+#define DEC_MMA_MIN 4
+#endif
+constexpr int DEC_GPW = DEC_GPW_;   // groups a wave keeps in flight at once
+
+// MP >= 4 runs the dot products on the matrix core: per 16 k-bytes one v_mfma_i32_32x32x32_i8 with the weights as
+// the B operand straight from the tile layout (lane l holds row l; column j of B is row j in the low k-half and row
+// j + 32 in the high k-half) and the activations as A: row i < MP of A is token i in the low k-half (zero in the high
+// one), row MP + i is token i in the high k-half (zero in the low one).  Element (i, j) of the 32 x 32 result
+// (lane j + 32 * ((i / 4) % 2), register 4 * (i / 8) + i % 4) is then the partial sum of token i mod MP with weight
+// row j + 32 * (i >= MP); registers r < MP carry every (row, token) pair of the tile once.
+template <int MP>
+__device__ __forceinline__ int dec_tok(int r, int lane) {
+    if (MP < DEC_MMA_MIN) return r;
+    const int i = 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+    return i >= MP ? i - MP : i;
+}
+template <int MP>
+__device__ __forceinline__ int dec_row(int r, int lane) {
+    if (MP < DEC_MMA_MIN) return lane;
+    const int i = 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+    return (lane & 31) + (i >= MP ? 32 : 0);
+}
+
+template <int MP>
+constexpr int dec_maxw() { return MP >= DEC_MMA_MIN ? 8 : DEC_MAXW; }     // the matrix-core form needs up to 256 VGPRs
 
 template <int BITS, int MP>
-__global__ void __launch_bounds__(64 * DEC_MAXW) k_decode(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
+__global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                 const uint16_t* __restrict__ ms, int N, int K,
                                                 const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                const uint16_t* __restrict__ mx, int M, Out out) {
+                                                const uint16_t* __restrict__ mx, int M, Out out, int KS,
+                                                long long* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int NC = group_bytes(BITS) / 16;     // 16-byte chunks per row-group
+    constexpr bool MMA = MP >= DEC_MMA_MIN;
+    static_assert(MP <= 16, "at most 16 tokens");
     extern __shared__ long long red_dyn[];          // [S][MP][64] int64 partial sums
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, S = blockDim.x >> 6;
-    const int tile = blockIdx.x;
+    __shared__ unsigned int last_s;
+    const int lane = threadIdx.x & 63, S = blockDim.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     // wave-uniform: activations come in by scalar loads
+    const int tile = blockIdx.x / KS, ks = blockIdx.x - tile * KS;
     const int G = K / GROUP;
+    const int gs = (G + KS - 1) / KS;              // groups per slice
+    const int g0 = ks * gs, g1 = min(G, g0 + gs);
     long long acc[MP];
 #pragma unroll
     for (int t = 0; t < MP; t++) acc[t] = 0;
+    // matrix-core path: the token whose activations this lane feeds into A (-1: none)
+    const int ai = lane & 31;
+    int atok = (lane < 32) ? (ai < MP ? ai : -1) : (ai >= MP && ai < 2 * MP ? ai - MP : -1);
+    if (atok >= M) atok = -1;
 
-    for (int g = wv; g < G; g += S) {
-        const size_t tg = (size_t)tile * G + g;
-        const uint4* src = reinterpret_cast<const uint4*>(wq + tg * NC * 1024) + lane;
-        uint32_t q[NC * 4];
+    for (int gb = g0 + wv; gb < g1; gb += S * DEC_GPW) {
+        uint32_t q[DEC_GPW][NC * 4];
+        uint32_t mm[DEC_GPW][MMA ? 2 : 1];
+        v4i xa[MMA ? DEC_GPW : 1][MMA ? 8 : 1];
+        uint32_t mxa[DEC_GPW];
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
-            const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src + c * 64));
-            q[4 * c] = v.x; q[4 * c + 1] = v.y; q[4 * c + 2] = v.z; q[4 * c + 3] = v.w;
+        for (int u = 0; u < DEC_GPW; u++) {          // every load of this batch before any arithmetic
+            const int g = gb + u * S;
+            if (g < g1) {
+                const size_t tg = (size_t)tile * G + g;
+                const v4i* src = reinterpret_cast<const v4i*>(wq + tg * NC * 1024) + lane;
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const v4i v = __builtin_nontemporal_load(src + c * 64);
+                    q[u][4 * c] = v.x; q[u][4 * c + 1] = v.y; q[u][4 * c + 2] = v.z; q[u][4 * c + 3] = v.w;
+                }
+                if constexpr (MMA) {
+                    mm[u][0] = ms[tg * 64 + (lane & 31)];
+                    mm[u][1] = ms[tg * 64 + (lane & 31) + 32];
+                    const v4i z = {0, 0, 0, 0};
+                    const v4i* xs = reinterpret_cast<const v4i*>(xq + (size_t)max(atok, 0) * K + (size_t)g * GROUP);
+#pragma unroll
+                    for (int c = 0; c < 8; c++) xa[u][c] = atok >= 0 ? xs[c] : z;
+                    mxa[u] = atok < 0 ? 0u : (mx ? (uint32_t)mx[(size_t)atok * G + g] : 1u);
+                } else {
+                    mm[u][0] = ms[tg * 64 + lane];
+                }
+            }
         }
-        const uint32_t mm = ms[tg * 64 + lane];
-        uint32_t w[32];
 #pragma unroll
-        for (int b = 0; b < 4; b++) block_signed<BITS>(q + b * NC, w + 8 * b);
+        for (int u = 0; u < DEC_GPW; u++) {
+            const int g = gb + u * S;
+            if (g < g1) {
+                uint32_t w[32];
 #pragma unroll
-        for (int t = 0; t < MP; t++) {
-            if (t < M) {
-                const int* xr = reinterpret_cast<const int*>(xq + (size_t)t * K + (size_t)g * GROUP);
-                int p = 0;
+                for (int b = 0; b < 4; b++) block_signed<BITS>(q[u] + b * NC, w + 8 * b);
+                if constexpr (MMA) {
+                    v16i d = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-                for (int j = 0; j < 32; j++) p = __builtin_amdgcn_sdot4((int)w[j], xr[j], p, false);
-                const uint32_t s = mm * (mx ? (uint32_t)mx[(size_t)t * G + g] : 1u);
-                mac_s32_u32(acc[t], p, s);
+                    for (int c = 0; c < 8; c++) {
+                        const v4i bw = {(int)w[4 * c], (int)w[4 * c + 1], (int)w[4 * c + 2], (int)w[4 * c + 3]};
+                        d = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[u][c], bw, d, 0, 0, 0);
+                    }
+                    // multipliers of token t: lane t feeds token t (t < MP), so read them across the wave
+                    uint32_t mxt[MP];
+#pragma unroll
+                    for (int t = 0; t < MP; t++) mxt[t] = __builtin_amdgcn_readlane(mxa[u], t);
+#pragma unroll
+                    for (int r = 0; r < MP; r++) {
+                        // token and row of register r in the low and high half of the wave (compile-time per half)
+                        const int i0 = 8 * (r / 4) + (r % 4), i1 = i0 + 4;
+                        const uint32_t mx0 = mxt[i0 >= MP ? i0 - MP : i0], mx1 = mxt[i1 >= MP ? i1 - MP : i1];
+                        const uint32_t m0 = mm[u][i0 >= MP], m1 = mm[u][i1 >= MP];
+                        const uint32_t sc = lane < 32 ? m0 * mx0 : m1 * mx1;
+                        mac_s32_u32(acc[r], d[r], sc);
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < MP; t++) {
+                        if (t < M) {
+                            const int* xr = reinterpret_cast<const int*>(xq + (size_t)t * K + (size_t)g * GROUP);
+                            int p = 0;
+#pragma unroll
+                            for (int j = 0; j < 32; j++) p = __builtin_amdgcn_sdot4((int)w[j], xr[j], p, false);
+                            const uint32_t sc = mm[u][0] * (mx ? (uint32_t)mx[(size_t)t * G + g] : 1u);
+                            mac_s32_u32(acc[t], p, sc);
+                        }
+                    }
+                }
             }
         }
     }
-    const int n = tile * TILE_N + lane;
-    if (S == 1) {
-        if (n < N) {
-            const float c = cs[n];
+    // register r of this lane holds (token dec_tok(r), row dec_row(r)); tokens >= M are padding
+    if (S == 1 && KS == 1) {
 #pragma unroll
-            for (int t = 0; t < MP; t++)
-                if (t < M) out.store(N, t, n, (i64_to_f(acc[t]) * c) * sx[t]);
+        for (int r = 0; r < MP; r++) {
+            const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
+            if (t < M && n < N) out.store(N, t, n, (i64_to_f(acc[r]) * cs[n]) * sx[t]);
         }
         return;
     }
+    if (S > 1) {
 #pragma unroll
-    for (int t = 0; t < MP; t++) red_dyn[(wv * MP + t) * 64 + lane] = acc[t];
-    __syncthreads();
-    if (n < N) {
-        for (int t = wv; t < M && t < MP; t += S) {
-            long long tot = 0;
-            for (int w = 0; w < S; w++) tot += red_dyn[(w * MP + t) * 64 + lane];
-            out.store(N, t, n, (i64_to_f(tot) * cs[n]) * sx[t]);
+        for (int r = 0; r < MP; r++) red_dyn[(wv * MP + r) * 64 + lane] = acc[r];
+        __syncthreads();
+    }
+    // wave w finishes registers w, w + S, ... of the workgroup's sum
+    const size_t npad = (size_t)(gridDim.x / KS) * TILE_N;
+    long long tot[MP];
+#pragma unroll
+    for (int r = 0; r < MP; r++) {
+        tot[r] = 0;
+        const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
+        if (r % S != wv) continue;
+        long long v = 0;
+        if (S > 1) for (int w = 0; w < S; w++) v += red_dyn[(w * MP + r) * 64 + lane];
+        else v = acc[r];
+        tot[r] = v;
+        // every slice adds into the accumulator (device-coherent atomics: no cache write-back needed)
+        if (KS > 1 && t < M) __hip_atomic_fetch_add(part + (size_t)t * npad + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (KS > 1) {
+        __builtin_amdgcn_s_waitcnt(0);             // this wave's adds have been performed
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);
+        __syncthreads();
+        if (!last_s) return;
+        // the last slice to arrive reads the sums, leaving the accumulator and the counter at zero for the next call
+#pragma unroll
+        for (int r = 0; r < MP; r++) {
+            const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
+            if (r % S != wv || t >= M) continue;
+            tot[r] = __hip_atomic_exchange(part + (size_t)t * npad + n, 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int r = 0; r < MP; r++) {
+        const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
+        if (r % S == wv && t < M && n < N) out.store(N, t, n, (i64_to_f(tot[r]) * cs[n]) * sx[t]);
     }
 }
 
-// ------------------------------------------------------------------ MFMA GEMM (M > 8)
+// ------------------------------------------------------------------ MFMA GEMM (16 < M <= 64)
 constexpr int MF_BN = 128;          // output rows n per workgroup (two 64-row tiles)
 constexpr int MF_STR = 144;         // LDS row stride in bytes (128 codes + 16 pad)
 
@@ -771,7 +892,7 @@ __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ w, i
 // ------------------------------------------------------------------ host side
 int g_num_cus = 0;
 int g_decode_waves = 2048;      // target waves per decode launch (split-K below it)
-int g_decode_max_m = 8;
+int g_decode_max_m = 16;
 // Per-(token, group) first accumulators of the W4/W6 prefill path, M * (K/128) int32: normally the buffer registered
 // with det_gemm_set_scratch; without one (or with a too small one) a lazily grown global buffer, as in the reference
 // (gemm.cu:913-936): a one-time note on stderr, and only safe when all det_gemm calls are ordered on one stream.
@@ -799,15 +920,53 @@ int* cinit_scratch(int M, int G, hipStream_t st) {
     return g_cinit;
 }
 
+// K-split buffers of k_decode: int64 accumulators part[MP][Npad] and per-tile arrival counters, zero between calls
+// (the last workgroup of each tile clears what it used); library-owned, grown on demand.  Calls that overlap on
+// different streams would share them: det runs every call on one in-order stream.
+long long* g_part = nullptr;
+size_t g_part_cap = 0;              // elements
+unsigned int* g_cnt = nullptr;
+size_t g_cnt_cap = 0;
+
+void decode_buffers(size_t part_elems, size_t tiles, hipStream_t st) {
+    if (part_elems <= g_part_cap && tiles <= g_cnt_cap) return;
+    DET_CHECK(hipStreamSynchronize(st));     // earlier launches may still use the old buffers
+    if (part_elems > g_part_cap) {
+        if (g_part) DET_CHECK(hipFree(g_part));
+        g_part_cap = std::max(part_elems, (size_t)1 << 20);
+        DET_CHECK(hipMalloc(&g_part, g_part_cap * 8));
+        DET_CHECK(hipMemset(g_part, 0, g_part_cap * 8));
+    }
+    if (tiles > g_cnt_cap) {
+        if (g_cnt) DET_CHECK(hipFree(g_cnt));
+        g_cnt_cap = std::max(tiles, (size_t)1 << 14);
+        DET_CHECK(hipMalloc(&g_cnt, g_cnt_cap * 4));
+        DET_CHECK(hipMemset(g_cnt, 0, g_cnt_cap * 4));
+    }
+    DET_CHECK(hipDeviceSynchronize());
+}
+
 template <int BITS, int MP>
 void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
     const int G = L.K / GROUP;
     const int T = (L.N + TILE_N - 1) / TILE_N;
-    // waves per tile: enough to put ~g_decode_waves waves in flight, at most one per group and DEC_MAXW
-    int S = (g_decode_waves + T - 1) / T;
-    S = std::max(1, std::min(S, std::min(G, DEC_MAXW)));
+    // K-split only when the tiles cannot occupy half the CUs: the split's combine costs three dependent memory round
+    // trips, which a launch that already fills the device does not repay.
+    const int cus = g_decode_waves / 8;
+    int KS = 1;
+    if (2 * T < cus) KS = std::max(1, std::min((cus + T - 1) / T, (G + 3) / 4));
+    const int gs = (G + KS - 1) / KS;
+    int S = (g_decode_waves + T * KS - 1) / (T * KS);
+    S = std::max(1, std::min(S, std::min(gs, std::min(dec_maxw<MP>(), 128 / MP))));     // LDS: S * MP * 512 <= 64 KB
+    long long* part = nullptr;
+    unsigned int* cnt = nullptr;
+    if (KS > 1) {
+        decode_buffers((size_t)MP * T * TILE_N, (size_t)T, st);
+        part = g_part;
+        cnt = g_cnt;
+    }
     const size_t lds = S > 1 ? (size_t)S * MP * 64 * sizeof(long long) : 0;
-    k_decode<BITS, MP><<<T, 64 * S, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y);
+    k_decode<BITS, MP><<<T * KS, 64 * S, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
     DET_CHECK(hipGetLastError());
 }
 
@@ -822,9 +981,9 @@ template <int BITS>
 void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
     if (M <= g_decode_max_m) {
         if (M <= 1) launch_decode<BITS, 1>(L, xq, sx, mx, M, y, st);
-        else if (M <= 2) launch_decode<BITS, 2>(L, xq, sx, mx, M, y, st);
         else if (M <= 4) launch_decode<BITS, 4>(L, xq, sx, mx, M, y, st);
-        else launch_decode<BITS, 8>(L, xq, sx, mx, M, y, st);
+        else if (M <= 8) launch_decode<BITS, 8>(L, xq, sx, mx, M, y, st);
+        else launch_decode<BITS, 16>(L, xq, sx, mx, M, y, st);
     } else if (M <= 64) {
         launch_mfma<BITS, 64>(L, xq, sx, mx, M, y, st);
     } else {

@@ -157,12 +157,13 @@ def test_int64_to_fp32_ties():
     lin = ffi.Linear(rows, K, 8)
     got = run_gemm(lin, xq, sx, mx, 1)
     assert same_f32(want, got) is None
-    # the same columns through the MFMA path (M > 8): repeat the token
-    xq9 = np.repeat(xq, 9, axis=0)
-    mx9 = np.repeat(mx, 9, axis=0)
-    sx9 = np.ones(9, np.float32)
-    want9 = oracle.gemm(rows, N, K, 8, xq9, sx9, mx9)
-    assert same_f32(want9, run_gemm(lin, xq9, sx9, mx9, 9)) is None
+    # the same columns through the matrix-core paths (decode M = 9, tiled M = 20): repeat the token
+    for M in (9, 20):
+        xqm = np.repeat(xq, M, axis=0)
+        mxm = np.repeat(mx, M, axis=0)
+        sxm = np.ones(M, np.float32)
+        wantm = oracle.gemm(rows, N, K, 8, xqm, sxm, mxm)
+        assert same_f32(wantm, run_gemm(lin, xqm, sxm, mxm, M)) is None, f'M={M}'
 
 
 @pytest.mark.parametrize('bits,code', [(8, 127), (8, -127), (8, -128), (6, 31), (6, -32), (4, 7), (4, -8)])
@@ -193,3 +194,21 @@ def test_baseline_w6_9728x2560(M):
     xq, sx, mx = oracle.quant(x)
     want = oracle.gemm(rows, N, K, 6, xq, sx, mx)
     assert same_f32(want, run_gemm(lin, xq, sx, mx, M)) is None
+
+
+@pytest.mark.parametrize('bits', [8, 6, 4])
+def test_decode_every_m(bits):
+    """Every small batch M = 1..17 (each decode variant: dot-product M = 1, matrix-core M = 2..16, tiled 17), on a
+    shape whose tiles are few (split over K, int64 atomics across workgroups) and one whose tiles fill the device;
+    group and per-row activation scales; repeated calls, so the split's accumulators must come back to zero."""
+    rng = oracle.Rng(300 + bits)
+    for n, k in ((200, 3072), (9000, 512)):
+        rows = rng.fake_rows(bits, n, k)
+        lin = ffi.Linear(rows, k, bits)
+        for m in range(1, 18):
+            x = rng.acts_x(m, k)
+            for group in (True, False):
+                print(f'decode W{bits} n={n} k={k} m={m} group={group}', flush=True)
+                xq, sx, mx = oracle.quant(x, group=group)
+                want = oracle.gemm(rows, n, k, bits, xq, sx, mx)
+                assert same_f32(want, run_gemm(lin, xq, sx, mx, m)) is None, f'n={n} m={m} group={group}'
