@@ -36,10 +36,13 @@ struct Out {
     float* dst[4];
     __device__ __forceinline__ float* ptr(int N, int t, int n) const {
         if (nparts <= 1) return y + (size_t)t * N + n;
-        int i = 0;
+        // selects, not an indexed load: a runtime index into dst/offs would put the struct in private memory
+        float* d = dst[0];
+        int lo = offs[0], hi = offs[1];
 #pragma unroll
-        for (int j = 1; j < 4; j++) if (j < nparts && n >= offs[j]) i = j;
-        return dst[i] + (size_t)t * (offs[i + 1] - offs[i]) + (n - offs[i]);
+        for (int j = 1; j < 4; j++)
+            if (j < nparts && n >= offs[j]) { d = dst[j]; lo = offs[j]; hi = offs[j + 1]; }
+        return d + (size_t)t * (hi - lo) + (n - lo);
     }
     __device__ __forceinline__ void store(int N, int t, int n, float v) const {
         float* p = ptr(N, t, n);
@@ -421,10 +424,14 @@ __global__ void __launch_bounds__(256) k_mfma(const uint8_t* __restrict__ wq, co
 // ------------------------------------------------------------------ prefill MFMA GEMM (M > 64)
 // Workgroup tile 128 tokens x 128 rows, 4 waves of 64 x 64 (2 x 2 v_mfma_i32_32x32x32_i8 tiles), two workgroups
 // per CU.  LDS holds two buffers of the activation tile and of the signed int8 weight tile, 128 rows of 128 bytes
-// each, with the 16-byte chunk c of row r stored at position c ^ (r & 7) so that the fragment reads of 32 rows
-// spread over all banks.  Per 128-group, while the MFMAs run on one buffer, the next group's activations (and W8
-// codes) are copied global -> LDS by global_load_lds_dwordx4 into the other buffer; W4/W6 codes land in a packed
-// staging area that the same wave then unpacks into the other buffer (so one barrier per group suffices).
+// each, with the 16-byte chunk c of row r stored at position c ^ ((r / 2) % 8), so that the 16 rows one LDS cycle
+// serves fall on distinct banks.  Per 128-group, while the MFMAs run on one buffer, the next group's activations
+// (and W8 codes) are copied global -> LDS by the buffer unit (buffer_load_dwordx4 ... lds, in runs of up to four
+// 1 KB copies under one M0 value) into the other buffer; W4/W6 codes land in a packed staging area that the same
+// wave unpacks into the other buffer (so one barrier per group suffices).  The activation run is issued before the
+// group's MFMAs, the weight run halfway through them.
+//
+// Build with -DPF_TRACE to record per-phase timestamps of four workgroups (det_debug_trace) for profiling.
 //
 // Group scaling with two VALU ops per (token, row, group): the first MFMA of a group starts from a constant
 // accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
@@ -443,12 +450,75 @@ __device__ __forceinline__ void digits16(uint32_t v, int& d1, int& d0) {
     d1 = (vp - d0) >> 8;
 }
 // byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// (chunk position c ^ ((r / 2) % 8): the 16 rows that one LDS cycle serves fall on 16 distinct 16-byte bank slots)
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
-__device__ __forceinline__ void lds_load16(const void* g, void* l) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+// Global -> LDS copy by the buffer unit (BYTES = 4 or 16 per lane, lane i's bytes land at lds + i * BYTES), written as
+// inline assembly so that the compiler does not track it: with the builtin it cannot tell that later LDS reads touch
+// other buffers and waits for every copy in flight before the first of them.  The caller waits (s_waitcnt vmcnt)
+// and synchronises before reading the target.  `lds` must be wave-uniform.
+template <int BYTES>
+__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff_, const void* lds) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
+    if (BYTES == 16)
+        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
 }
 
+// N (<= 4) copies of 16 bytes per lane under one M0 value: copy i reads the resource at voff[i] + soff + 1024 i and
+// lands at lds + 1024 i + 16 lane (the instruction offset moves both addresses).  Changing M0 stalls until the copies
+// issued before have consumed it, so each run sets it once.
+template <int N>
+__device__ __forceinline__ void dma16_run(__amdgpu_buffer_rsrc_t r, const uint32_t* voff, uint32_t soff_, const void* lds) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);      // uniform by construction; keep it scalar
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
+    static_assert(N >= 1 && N <= 4, "at most 4 copies per run");
+    if constexpr (N == 4)
+        asm volatile("s_mov_b32 m0, %5\n\t"
+                     "buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
+                     "buffer_load_dwordx4 %1, %4, %6 offen offset:1024 lds\n\t"
+                     "buffer_load_dwordx4 %2, %4, %6 offen offset:2048 lds\n\t"
+                     "buffer_load_dwordx4 %3, %4, %6 offen offset:3072 lds"
+                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+    else if constexpr (N == 3)
+        asm volatile("s_mov_b32 m0, %4\n\t"
+                     "buffer_load_dwordx4 %0, %3, %5 offen lds\n\t"
+                     "buffer_load_dwordx4 %1, %3, %5 offen offset:1024 lds\n\t"
+                     "buffer_load_dwordx4 %2, %3, %5 offen offset:2048 lds"
+                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+    else if constexpr (N == 2)
+        asm volatile("s_mov_b32 m0, %3\n\t"
+                     "buffer_load_dwordx4 %0, %2, %4 offen lds\n\t"
+                     "buffer_load_dwordx4 %1, %2, %4 offen offset:1024 lds"
+                     :: "v"(voff[0]), "v"(voff[1]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\t"
+                     "buffer_load_dwordx4 %0, %1, %3 offen lds"
+                     :: "v"(voff[0]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+}
+// four copies under one M0, copy i through resource r[i] at voff[i % 2] + soff + 1024 i, landing at
+// lds + 1024 i + 16 lane
+__device__ __forceinline__ void dma16_run4x(const __amdgpu_buffer_rsrc_t* r, uint32_t voff0, uint32_t voff1, uint32_t soff_,
+                                            const void* lds) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %6\n\t"
+                 "buffer_load_dwordx4 %0, %2, %7 offen lds\n\t"
+                 "buffer_load_dwordx4 %1, %3, %7 offen offset:1024 lds\n\t"
+                 "buffer_load_dwordx4 %0, %4, %7 offen offset:2048 lds\n\t"
+                 "buffer_load_dwordx4 %1, %5, %7 offen offset:3072 lds"
+                 :: "v"(voff0), "v"(voff1), "s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[3]), "s"(m0v), "s"(soff) : "memory", "m0");
+}
+
+#ifdef PF_TRACE
+__device__ unsigned long long g_trace[4 * 64 * 8];
+#define PF_TR(slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
+    __builtin_amdgcn_sched_barrier(0); if (blockIdx.x < 4 && threadIdx.x == 0 && tr_hi < 64) g_trace[(blockIdx.x * 64 + tr_hi) * 8 + (slot)] = tr_; } while (0)
+#else
+#define PF_TR(slot) do {} while (0)
+#endif
 template <int BITS>
 __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                       const uint16_t* __restrict__ ms, int N, int K,
@@ -466,7 +536,6 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     // multipliers of the buffer's group: [0, 128) mx[t][g] of the tile's tokens, [128, 256) m[n][g] of its rows
     __shared__ __attribute__((aligned(16))) uint32_t mul0[PF_BM + PF_BN], mul1[PF_BM + PF_BN];
     __shared__ __attribute__((aligned(16))) int cis0[PF_BM], cis1[PF_BM];        // first accumulator per token (W4/W6)
-    __shared__ __attribute__((aligned(16))) int pf_sink[64];           // target of the L2 prefetch copies (never read)
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wvu = __builtin_amdgcn_readfirstlane(wv);        // the wave index as a scalar
@@ -481,6 +550,9 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     const int tile0 = n0 / TILE_N;
     const int l32 = lane & 31, lh = lane >> 5;
 
+    int tr_hi = 63;        // half-iteration index of the trace build (63: prologue and epilogue)
+    (void)tr_hi;
+    PF_TR(4);
     unsigned long long U[2][2][16];
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -505,73 +577,56 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     const bool x_one = xw && !(mx && t0 + tid < M);
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc((void*)cinit, (short)0, cinit ? M * G * 4 : 0, 0x00020000);
     const uint32_t c_vo = (uint32_t)(t0 + (tid & 127)) * (uint32_t)G * 4;     // rows past M: out of range, zero
-    uint32_t sreg = 1;
     int rsum = 0;          // Ra (tid < 128) or Rb (tid >= 128): sum over groups of (multiplier - 32896)
 
-    // Global -> LDS copies use buffer resources: one 32-bit per-lane offset, the rest in scalar offsets, and the
-    // hardware range check returns zeros for token rows past M.
-    // one resource per 8-row step i (base row + 8 i), so the per-lane offset is a single register and rows past M
-    // fall outside the resource's range
+    // Global -> LDS copies by the buffer unit, in runs that share one M0 value.  Activations: one resource over xq,
+    // copy i of wave wv takes rows t0 + 32 wv + 8 i + lane / 8 into As + 4096 wv + 1024 i (row r's chunk positions
+    // swizzled by r % 8); the hardware range check returns zeros for rows past M.
+    // Copy i reads through its own resource, based 8 i rows further on minus the 1 KB instruction offset, so all four
+    // share one per-lane offset; its range ends at row M (rows past M read as zero).
     __amdgpu_buffer_rsrc_t xr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        xr[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(xq + (size_t)i * 8 * K), (short)0, max(0, (M - 8 * i) * K), 0x00020000);
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, 2 * G * NC * 1024, 0x00020000);
-    // activations: wave wv fills rows 32*wv .. 32*wv+31 (4 x 64 slots of 16 bytes); slot p holds chunk
-    // (p % 8) ^ (row % 8) of row p / 8, and row % 8 == (lane / 8) % 8 for every slot of this lane
-    const uint32_t a_vo = (uint32_t)(t0 + wv * 32 + (lane >> 3)) * (uint32_t)K + (uint32_t)(((lane & 7) ^ ((lane >> 3) & 7)) * 16);
-    // W8 codes: slot p = row r * 8 + position q takes chunk q ^ (r & 7) of row r, r = 32 * (wv & 1) + 8 i + lane / 8
-    // within tile wv >> 1
-    const uint32_t b_vo = BITS == 8 ? (uint32_t)(((lane & 7) ^ ((lane >> 3) & 7)) * 1024 + (lane >> 3) * 16) : (uint32_t)lane * 16;
-
-    // L2 prefetch offsets: waves 0-1 cover the 2 * NC * 8 lines (128 bytes) of the tile pair's group (line L of
-    // tile L / (8 NC)), waves 2-3 one line of each of the 128 token rows
-    uint32_t pf_vo;
-    if (xw) {
-        const int L = wv * 64 + lane, lt = L / (NC * 8), lw = L - lt * (NC * 8);
-        pf_vo = lt < 2 ? (uint32_t)((lt * G * NC) * 1024 + lw * 128) : 0u;
-    } else {
-        pf_vo = (uint32_t)(t0 + (wv - 2) * 64 + lane) * (uint32_t)K;     // rows past M: out of range
-    }
-    // copy group g into (As, Bs / Bp) and its multiplier into sreg; nothing waits here
-    auto issue = [&](int g, int8_t* As, int8_t* Bs, int* cis) {
+        xr[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(xq + (size_t)i * 8 * K - 1024 * i), (short)0,
+                                                  M > 8 * i ? (M - 8 * i) * K + 1024 * i : 0, 0x00020000);
+    // LDS row R = 32 wv + 8 i + lane / 8 keeps chunk (lane % 8) ^ ((R / 2) % 8) = (lane % 8) ^ (lane / 16) ^ 4 (i % 2)
+    const uint32_t a_vo = (uint32_t)(t0 + wv * 32 + (lane >> 3)) * (uint32_t)K + (uint32_t)(((lane & 7) ^ (lane >> 4)) * 16);
+    const uint32_t a_vo1 = a_vo ^ 64u;          // odd copies: chunk bit 2 flipped (a_vo's low 7 bits are the chunk)
+    // weights: W8 copy i of wave wv (tile wv / 2, rows 32 (wv % 2) + 8 i + lane / 8) into Bs + 4096 wv + 1024 i; the
+    // resource starts 4 KB before the tile pair so that the per-copy offsets stay non-negative.  W4/W6: the wave's
+    // NC/2 chunk planes of its tile, consecutive 1 KB in memory and in Bp.
+    const __amdgpu_buffer_rsrc_t wr = BITS == 8
+        ? __builtin_amdgcn_make_buffer_rsrc((void*)(wbase - 4096), (short)0, 2 * G * NC * 1024 + 4096, 0x00020000)
+        : __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, 2 * G * NC * 1024, 0x00020000);
+    uint32_t b_voff[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr[i], (__attribute__((address_space(3))) void*)(As + (wvu * 256 + i * 64) * 16), 16,
-                                                     a_vo, g * GROUP, 0, 0);
-        if (BITS == 8) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(Bs + (wvu * 256 + i * 64) * 16), 16,
-                                                         b_vo, (((wvu >> 1) * G + g) * NC) * 1024 + ((wvu & 1) * 32 + i * 8) * 16, 0, 0);
-        } else {
-#pragma unroll
-            for (int c = 0; c < NC / 2; c++) {
-                const int cc = (wvu & 1) * (NC / 2) + c;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(Bp + ((wvu >> 1) * NC + cc) * 1024), 16,
-                                                         b_vo, (((wvu >> 1) * G + g) * NC + cc) * 1024, 0, 0);
-            }
-        }
+    for (int i = 0; i < 4; i++)
+        b_voff[i] = BITS == 8 ? (uint32_t)(4096 + ((lane & 7) ^ (lane >> 4) ^ (4 * (i & 1))) * 1024 + (lane >> 3) * 16 + (wv & 1) * 512 + 128 * i - 1024 * i)
+                              : (uint32_t)lane * 16;
+    // registers filled by the copies of one group: the thread's multiplier and its token's first accumulator (W4/W6)
+    uint32_t sreg = 1;
+    // copies of group g, in two runs with their own M0 value: the activations (issued first), then the weight codes,
+    // multiplier and first accumulators (issued halfway through the current group's MFMAs, when the first run has long
+    // consumed M0 and the new value does not stall); nothing waits here
+    auto issue_a = [&](int g, int8_t* As) {
+        dma16_run4x(xr, a_vo, a_vo1, g * GROUP, As + wvu * 4096);
+    };
+    auto issue_w = [&](int g, int8_t* Bs, int* cis) {
+        if (BITS == 8)
+            dma16_run<4>(wr, b_voff, ((wvu >> 1) * G + g) * NC * 1024, Bs + wvu * 4096);
+        else
+            dma16_run<NC / 2>(wr, b_voff, (((wvu >> 1) * G + g) * NC + (wvu & 1) * (NC / 2)) * 1024,
+                              Bp + ((wvu >> 1) * NC + (wvu & 1) * (NC / 2)) * 1024);
+        // a compiler-tracked load: an asm load's destination may be copied by the compiler before the data lands
         sreg = __builtin_amdgcn_raw_buffer_load_b16(sr, s_vo, g * s_step, 0);
         if (BITS != 8 && xw)   // W4/W6 first accumulators straight into LDS (waves 0 and 1: 64 tokens each)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(cr, (__attribute__((address_space(3))) void*)(cis + wvu * 64), 4, c_vo, g * 4, 0, 0);
-        // L2 prefetch of group g + 1 (the group after the one copied here): one dword per 128-byte line, waves 0-1
-        // the weight tiles, waves 2-3 the activation rows.  It is the last memory op of the wave, so the group's own
-        // copies are complete at vmcnt(1).
-        {
-            const int gp = min(g + 1, G - 1);
-            if (xw)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)pf_sink, 4,
-                                                         pf_vo, gp * NC * 1024, 0, 0);
-            else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr[0], (__attribute__((address_space(3))) void*)pf_sink, 4,
-                                                         pf_vo, gp * GROUP, 0, 0);
-        }
+            dma_lds<4>(cr, c_vo, g * 4, cis + wvu * 64);
     };
-    // wait for this wave's copies, stage the multiplier, unpack W4/W6 codes into Bs
+    // wait for this wave's copies, stage the multiplier (and first accumulator), unpack W4/W6 codes into Bs
     auto finish = [&](int8_t* Bs, uint32_t* sdst, bool real) {
         __builtin_amdgcn_sched_barrier(0);       // keep the wait after the scaling arithmetic of compute()
-        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");   // everything but the trailing L2 prefetch
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(sreg) :: "memory");
+        PF_TR(3);
         const uint32_t v = x_one ? 1u : sreg;
         sdst[tid] = v;
         rsum += real ? (int)v - DIG_C : 0;
@@ -582,8 +637,8 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
             uint32_t q[2 * NC];
 #pragma unroll
             for (int c = 0; c < NC / 2; c++) {       // 16-byte chunk reads: a wave reads 1 KB contiguous
-                const uint4 v = *reinterpret_cast<const uint4*>(pl + c * 1024);
-                q[4 * c] = v.x; q[4 * c + 1] = v.y; q[4 * c + 2] = v.z; q[4 * c + 3] = v.w;
+                const uint4 v4 = *reinterpret_cast<const uint4*>(pl + c * 1024);
+                q[4 * c] = v4.x; q[4 * c + 1] = v4.y; q[4 * c + 2] = v4.z; q[4 * c + 3] = v4.w;
             }
 #pragma unroll
             for (int blk = 0; blk < 2; blk++) {
@@ -595,7 +650,7 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         }
     };
     // MFMA over one group from (As, Bs) and scaling into U
-    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss, const int* cis) {
+    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss, const int* cis, auto&& mid) {
         // W4/W6 tiles hold u = wq + OFF; their chains start from B - OFF * sum(x) of the token (staged per group in
         // cis), so that d = B + x . u - OFF * sum(x) = B + x . wq.  W8 chains start from B.  The start values of
         // token tile i are read right before its first two MFMAs, so only 16 of them are live at a time.
@@ -645,43 +700,81 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                         U[i][j][4 * q4 + e] += (unsigned long long)(uint32_t)d[j][4 * q4 + e] * sc;
                     }
             }
+            if (i == 0) mid();
         }
     };
 
     // The copy of the next group is issued unconditionally (past the last group it re-reads group G-1 into the
     // idle buffer), so each half-iteration is one basic block and the scheduling barriers hold.
-    issue(0, As0, Bs0, cis0);
+    issue_a(0, As0);
+    issue_w(0, Bs0, cis0);
     finish(Bs0, mul0, true);
     __syncthreads();
+    PF_TR(5);
     for (int g = 0; g < G; g += 2) {
-        issue(min(g + 1, G - 1), As1, Bs1, cis1);
-        compute(As0, Bs0, mul0, mul0 + PF_BM, cis0);
+        tr_hi = g;
+        PF_TR(0);
+        const int g1 = g + 1;          // nothing to copy after the last group
+        if (g1 < G) issue_a(g1, As1);
+        PF_TR(1);
+        compute(As0, Bs0, mul0, mul0 + PF_BM, cis0, [&] { if (g1 < G) issue_w(g1, Bs1, cis1); });
+        PF_TR(2);
         finish(Bs1, mul1, g + 1 < G);
+        PF_TR(4);
         __syncthreads();
+        PF_TR(5);
         if (g + 1 >= G) break;
-        issue(min(g + 2, G - 1), As0, Bs0, cis0);
-        compute(As1, Bs1, mul1, mul1 + PF_BM, cis1);
+        tr_hi = g + 1;
+        PF_TR(0);
+        const int g2 = g + 2;
+        if (g2 < G) issue_a(g2, As0);
+        PF_TR(1);
+        compute(As1, Bs1, mul1, mul1 + PF_BM, cis1, [&] { if (g2 < G) issue_w(g2, Bs0, cis0); });
+        PF_TR(2);
         finish(Bs0, mul0, g + 2 < G);
+        PF_TR(4);
         __syncthreads();
+        PF_TR(5);
     }
 
     // ---- bias correction and epilogue.  S = sum_g m * mx comes from balanced digits on the MFMA, 32 groups at a
     // time: the multipliers of those groups are staged in the (now idle) LDS buffers, xs[t][32] = mx and
     // ws[n][32] = m (uint16), and U -= B * (65536 D11 + 256 (D10 + D01) + D00) is applied per step (it is linear).
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");          // the last L2 prefetch copy has landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    tr_hi = 63;
+    PF_TR(0);
     uint16_t* xs = reinterpret_cast<uint16_t*>(As0);            // PF_BM * 32 * 2 = 8 KB
     uint16_t* ws = reinterpret_cast<uint16_t*>(Bs0);            // PF_BN * 32 * 2 = 8 KB
     int* Ra = reinterpret_cast<int*>(As1);                      // sums of (mx - 32896) per token
     int* Rb = Ra + PF_BM;                                       // sums of (m - 32896) per row
-    if (tid < PF_BM) Ra[tid] = rsum;
-    else Rb[tid - PF_BM] = rsum;
+    float* sxs = reinterpret_cast<float*>(Rb + PF_BN);          // sx of the tile's tokens
+    if (tid < PF_BM) {
+        Ra[tid] = rsum;
+        sxs[tid] = sx[min(t0 + tid, M - 1)];
+    } else {
+        Rb[tid - PF_BM] = rsum;
+    }
+    // staging of 32 groups: thread tid loads 16 of them for token tid / 2 and for row tid / 2 (half tid % 2), all
+    // loads first, then the LDS writes (packed in pairs)
+    const int sl = tid >> 1, sh = (tid & 1) * 16;
+    const bool tok_ok = mx && t0 + sl < M;
+    const uint16_t* mrow = mx + (size_t)(t0 + sl) * G;
+    const uint16_t* wrow = ms + (size_t)(tile0 + (sl >> 6)) * G * 64 + (sl & 63);
     for (int k0 = 0; k0 < G; k0 += 32) {
-        __syncthreads();
-        for (int e = tid; e < PF_BM * 32; e += 256) {
-            const int rl = e >> 5, g = k0 + (e & 31);
+        uint32_t xv[16], wv_[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int g = k0 + sh + e;
             // a multiplier of 32896 has zero digits: groups past G add nothing
-            xs[e] = g < G ? ((mx && t0 + rl < M) ? mx[(size_t)(t0 + rl) * G + g] : (uint16_t)1) : (uint16_t)DIG_C;
-            ws[e] = g < G ? ms[((size_t)(tile0 + (rl >> 6)) * G + g) * 64 + (rl & 63)] : (uint16_t)DIG_C;
+            xv[e] = g < G ? (tok_ok ? (uint32_t)mrow[g] : 1u) : (uint32_t)DIG_C;
+            wv_[e] = g < G ? (uint32_t)wrow[(size_t)g * 64] : (uint32_t)DIG_C;
+        }
+        PF_TR(6);
+        __syncthreads();                     // the previous chunk's digit reads are done
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+            *reinterpret_cast<uint32_t*>(xs + sl * 32 + sh + e) = xv[e] | (xv[e + 1] << 16);
+            *reinterpret_cast<uint32_t*>(ws + sl * 32 + sh + e) = wv_[e] | (wv_[e + 1] << 16);
         }
         __syncthreads();
         v4i A1[2], A0[2], B1[2], B0[2];
@@ -723,9 +816,11 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                 }
             }
     }
+    PF_TR(1);
     const long long GC2 = (long long)G * DIG_C * DIG_C;
-    // epilogue, 16 outputs at a time; Accumulate loads all 16 old values before the first store, so no store waits
-    // on a load
+    // epilogue, 16 outputs at a time.  A whole tile routed to one plain output needs no per-element checks;
+    // Accumulate loads all 16 old values before the first store, so no store waits on a load.
+    const bool full = t0 + PF_BM <= M && n0 + PF_BN <= N && out.nparts <= 1;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int nb = wn * 64 + j * 32 + l32;
@@ -736,29 +831,50 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         for (int i = 0; i < 2; i++) {
             float v[16];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int tr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const long long rest = (long long)DIG_C * (Ra[tr] + rb) + GC2;
-                const long long acc = (long long)(U[i][j][r] - ((unsigned long long)rest << 21));
-                v[r] = ((float)acc * cn) * sx[min(t0 + tr, M - 1)];   // int64 -> fp32 rounds to nearest even
+            for (int q4 = 0; q4 < 4; q4++) {
+                const int trb = wm * 64 + i * 32 + 8 * q4 + 4 * lh;
+                const int4 ra = *reinterpret_cast<const int4*>(Ra + trb);
+                const float4 sv = *reinterpret_cast<const float4*>(sxs + trb);
+                const int rav[4] = {ra.x, ra.y, ra.z, ra.w};
+                const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const long long rest = (long long)DIG_C * (rav[e] + rb) + GC2;
+                    const long long acc = (long long)(U[i][j][4 * q4 + e] - ((unsigned long long)rest << 21));
+                    v[4 * q4 + e] = ((float)acc * cn) * svv[e];   // int64 -> fp32 rounds to nearest even
+                }
             }
-            if (out.acc) {
-                float old[16];
+            if (full) {
+                float* yb = out.y + (size_t)(t0 + wm * 64 + i * 32 + 4 * lh) * N + n;
+                if (out.acc) {
+                    float old[16];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) old[r] = yb[(size_t)(8 * (r >> 2) + (r & 3)) * N];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++) yb[(size_t)(8 * (r >> 2) + (r & 3)) * N] = v[r];
+            } else {
+                if (out.acc) {
+                    float old[16];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        old[r] = (t < M && n < N) ? *out.ptr(N, t, n) : 0.0f;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
+                }
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    old[r] = (t < M && n < N) ? *out.ptr(N, t, n) : 0.0f;
+                    if (t < M && n < N) *out.ptr(N, t, n) = v[r];
                 }
-#pragma unroll
-                for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (t < M && n < N) *out.ptr(N, t, n) = v[r];
             }
         }
     }
+    PF_TR(2);
 }
 
 // First MFMA accumulator of each (token, group) for W4/W6: cinit[t][g] = 2^21 - OFF * sum_{k in g} xq[t][k]
@@ -1031,6 +1147,12 @@ void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hi
     DET_CHECK(hipGetLastError());
 }
 
+#ifdef PF_TRACE
+void det_debug_trace(unsigned long long* host) {
+    DET_CHECK(hipDeviceSynchronize());
+    DET_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace)));
+}
+#endif
 size_t det_gemm_scratch_bytes(int M, int K) { return (size_t)(M < 1 ? 1 : M) * (size_t)((K + 127) / 128) * sizeof(int); }
 void det_gemm_set_scratch(void* p, size_t bytes) { g_user_scratch = p; g_user_scratch_bytes = p ? bytes : 0; }
 
