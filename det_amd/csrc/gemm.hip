@@ -523,7 +523,7 @@ template <int BITS>
 __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                       const uint16_t* __restrict__ ms, int N, int K,
                                                       const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                      const uint16_t* __restrict__ mx, const int* __restrict__ cinit, int M,
+                                                      const uint16_t* __restrict__ mx, int M,
                                                       Out out, int nbn, int nbt) {
     constexpr int NC = group_bytes(BITS) / 16;
     constexpr int PK = BITS == 8 ? 16 : 2 * NC * 1024;         // packed staging bytes (W4/W6)
@@ -535,7 +535,6 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     __shared__ __attribute__((aligned(16))) uint8_t Bp[PK];
     // multipliers of the buffer's group: [0, 128) mx[t][g] of the tile's tokens, [128, 256) m[n][g] of its rows
     __shared__ __attribute__((aligned(16))) uint32_t mul0[PF_BM + PF_BN], mul1[PF_BM + PF_BN];
-    __shared__ __attribute__((aligned(16))) int cis0[PF_BM], cis1[PF_BM];        // first accumulator per token (W4/W6)
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wvu = __builtin_amdgcn_readfirstlane(wv);        // the wave index as a scalar
@@ -561,13 +560,13 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
 #pragma unroll
             for (int r = 0; r < 16; r++) U[i][j][r] = 0;
 
-    // weight copy: W8 straight into Bs (slot p = row r * 8 + position q takes chunk q ^ (r & 7) of row r),
+    // weight copy: W8 straight into Bs (slot p = row r * 8 + position q takes chunk q ^ ((r / 2) % 8) of row r),
     // W4/W6 into the Bp planes (wave wv: tile wv >> 1, chunk planes (wv & 1) * NC/2 .. +NC/2, which are exactly
     // the half-groups this wave unpacks itself).  Per-lane addresses are 32-bit offsets from uniform bases.
     const uint8_t* wbase = wq + (size_t)tile0 * G * NC * 1024;
     // per-group multipliers: thread tid < 128 (waves 0, 1) stages mx of token t0 + tid, the others (waves 2, 3) m of
     // row n0 + tid - 128, through buffer loads (the resource is uniform per wave); a missing mx (NULL) or a token
-    // past M reads as zero and stages 1.  W4/W6 also stage the token's first accumulator cinit[t][g].
+    // past M reads as zero and stages 1.
     const bool xw = wvu < 2;
     const __amdgpu_buffer_rsrc_t sr = xw ? __builtin_amdgcn_make_buffer_rsrc((void*)mx, (short)0, mx ? M * G * 2 : 0, 0x00020000)
                                          : __builtin_amdgcn_make_buffer_rsrc((void*)ms, (short)0, (tile0 + 2) * G * 128, 0x00020000);
@@ -575,8 +574,6 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                              : (uint32_t)((tile0 + ((tid - PF_BM) >> 6)) * G * 64 + ((tid - PF_BM) & 63)) * 2;
     const int s_step = xw ? 2 : 128;
     const bool x_one = xw && !(mx && t0 + tid < M);
-    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc((void*)cinit, (short)0, cinit ? M * G * 4 : 0, 0x00020000);
-    const uint32_t c_vo = (uint32_t)(t0 + (tid & 127)) * (uint32_t)G * 4;     // rows past M: out of range, zero
     int rsum = 0;          // Ra (tid < 128) or Rb (tid >= 128): sum over groups of (multiplier - 32896)
 
     // Global -> LDS copies by the buffer unit, in runs that share one M0 value.  Activations: one resource over xq,
@@ -605,13 +602,12 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                               : (uint32_t)lane * 16;
     // registers filled by the copies of one group: the thread's multiplier and its token's first accumulator (W4/W6)
     uint32_t sreg = 1;
-    // copies of group g, in two runs with their own M0 value: the activations (issued first), then the weight codes,
-    // multiplier and first accumulators (issued halfway through the current group's MFMAs, when the first run has long
-    // consumed M0 and the new value does not stall); nothing waits here
+    // copies of group g, in two runs with their own M0 value: the activations (issued first), then the weight codes
+    // and the multiplier (issued halfway through the current group's MFMAs); nothing waits here
     auto issue_a = [&](int g, int8_t* As) {
         dma16_run4x(xr, a_vo, a_vo1, g * GROUP, As + wvu * 4096);
     };
-    auto issue_w = [&](int g, int8_t* Bs, int* cis) {
+    auto issue_w = [&](int g, int8_t* Bs) {
         if (BITS == 8)
             dma16_run<4>(wr, b_voff, ((wvu >> 1) * G + g) * NC * 1024, Bs + wvu * 4096);
         else
@@ -619,10 +615,9 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                               Bp + ((wvu >> 1) * NC + (wvu & 1) * (NC / 2)) * 1024);
         // a compiler-tracked load: an asm load's destination may be copied by the compiler before the data lands
         sreg = __builtin_amdgcn_raw_buffer_load_b16(sr, s_vo, g * s_step, 0);
-        if (BITS != 8 && xw)   // W4/W6 first accumulators straight into LDS (waves 0 and 1: 64 tokens each)
-            dma_lds<4>(cr, c_vo, g * 4, cis + wvu * 64);
     };
-    // wait for this wave's copies, stage the multiplier (and first accumulator), unpack W4/W6 codes into Bs
+    // wait for this wave's copies, stage the multiplier and unpack W4/W6 codes into the signed-int8 tile Bs (the
+    // wave reads only the staging planes its own copies wrote); the barrier follows
     auto finish = [&](int8_t* Bs, uint32_t* sdst, bool real) {
         __builtin_amdgcn_sched_barrier(0);       // keep the wait after the scaling arithmetic of compute()
         asm volatile("s_waitcnt vmcnt(0)" : "+v"(sreg) :: "memory");
@@ -631,7 +626,6 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         sdst[tid] = v;
         rsum += real ? (int)v - DIG_C : 0;
         if (BITS != 8) {
-            // 64 codes = two 32-code blocks; each block's NC words sit in the wave's own staging planes
             const int r = (wv >> 1) * 64 + lane, h = wv & 1;
             const uint8_t* pl = Bp + ((wv >> 1) * NC + h * (NC / 2)) * 1024 + lane * 16;
             uint32_t q[2 * NC];
@@ -643,29 +637,19 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
 #pragma unroll
             for (int blk = 0; blk < 2; blk++) {
                 uint32_t o[8];
-                block_unsigned<BITS>(q + blk * NC, o);
+                block_signed<BITS>(q + blk * NC, o);
                 *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2)) = make_uint4(o[0], o[1], o[2], o[3]);
                 *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2 + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
             }
         }
     };
     // MFMA over one group from (As, Bs) and scaling into U
-    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss, const int* cis, auto&& mid) {
-        // W4/W6 tiles hold u = wq + OFF; their chains start from B - OFF * sum(x) of the token (staged per group in
-        // cis), so that d = B + x . u - OFF * sum(x) = B + x . wq.  W8 chains start from B.  The start values of
-        // token tile i are read right before its first two MFMAs, so only 16 of them are live at a time.
-        auto cinit_of = [&](int i) {
+    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss, auto&& mid) {
+        // every chain starts from the bias B (the tiles hold signed codes)
+        auto cinit_of = [&](int) {
             v16i c;
-            if (BITS != 8) {
 #pragma unroll
-                for (int q4 = 0; q4 < 4; q4++) {
-                    const int4 cv = *reinterpret_cast<const int4*>(cis + wm * 64 + i * 32 + 8 * q4 + 4 * lh);
-                    c[4 * q4] = cv.x; c[4 * q4 + 1] = cv.y; c[4 * q4 + 2] = cv.z; c[4 * q4 + 3] = cv.w;
-                }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; r++) asm volatile("v_mov_b32 %0, %1" : "=v"(c[r]) : "i"(PF_BIAS));
-            }
+            for (int r = 0; r < 16; r++) asm volatile("v_mov_b32 %0, %1" : "=v"(c[r]) : "i"(PF_BIAS));
             return c;
         };
         // one token tile at a time: its two n-tiles' MFMA chains (32 accumulator registers), then their scaling
@@ -707,7 +691,7 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     // The copy of the next group is issued unconditionally (past the last group it re-reads group G-1 into the
     // idle buffer), so each half-iteration is one basic block and the scheduling barriers hold.
     issue_a(0, As0);
-    issue_w(0, Bs0, cis0);
+    issue_w(0, Bs0);
     finish(Bs0, mul0, true);
     __syncthreads();
     PF_TR(5);
@@ -717,21 +701,21 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         const int g1 = g + 1;          // nothing to copy after the last group
         if (g1 < G) issue_a(g1, As1);
         PF_TR(1);
-        compute(As0, Bs0, mul0, mul0 + PF_BM, cis0, [&] { if (g1 < G) issue_w(g1, Bs1, cis1); });
+        compute(As0, Bs0, mul0, mul0 + PF_BM, [&] { if (g1 < G) issue_w(g1, Bs1); });
         PF_TR(2);
-        finish(Bs1, mul1, g + 1 < G);
+        finish(Bs1, mul1, g1 < G);
         PF_TR(4);
         __syncthreads();
         PF_TR(5);
-        if (g + 1 >= G) break;
-        tr_hi = g + 1;
+        if (g1 >= G) break;
+        tr_hi = g1;
         PF_TR(0);
         const int g2 = g + 2;
         if (g2 < G) issue_a(g2, As0);
         PF_TR(1);
-        compute(As1, Bs1, mul1, mul1 + PF_BM, cis1, [&] { if (g2 < G) issue_w(g2, Bs0, cis0); });
+        compute(As1, Bs1, mul1, mul1 + PF_BM, [&] { if (g2 < G) issue_w(g2, Bs0); });
         PF_TR(2);
-        finish(Bs0, mul0, g + 2 < G);
+        finish(Bs0, mul0, g2 < G);
         PF_TR(4);
         __syncthreads();
         PF_TR(5);
@@ -877,24 +861,6 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     PF_TR(2);
 }
 
-// First MFMA accumulator of each (token, group) for W4/W6: cinit[t][g] = 2^21 - OFF * sum_{k in g} xq[t][k]
-// (the prefill kernel multiplies unsigned codes u = wq + OFF; this restores x . wq and adds the bias B)
-__global__ void k_cinit(const int8_t* __restrict__ xq, int MG, int off, int* __restrict__ cinit) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;     // (t * G + g), and xq + idx * 128 is its group
-    if (idx >= MG) return;
-    const int4* p = reinterpret_cast<const int4*>(xq + (size_t)idx * GROUP);
-    int s = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int4 v = p[i];
-        s = __builtin_amdgcn_sdot4(v.x, 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4(v.y, 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
-    }
-    cinit[idx] = (int)PF_BIAS - off * s;
-}
-
 // ------------------------------------------------------------------ load-time repack and quantizer
 __global__ void k_repack(const uint8_t* __restrict__ rows, int N, int K, int bits, uint8_t* __restrict__ wq,
                          float* __restrict__ cs, uint16_t* __restrict__ ms, size_t nchunks) {
@@ -1009,32 +975,10 @@ __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ w, i
 int g_num_cus = 0;
 int g_decode_waves = 2048;      // target waves per decode launch (split-K below it)
 int g_decode_max_m = 16;
-// Per-(token, group) first accumulators of the W4/W6 prefill path, M * (K/128) int32: normally the buffer registered
-// with det_gemm_set_scratch; without one (or with a too small one) a lazily grown global buffer, as in the reference
-// (gemm.cu:913-936): a one-time note on stderr, and only safe when all det_gemm calls are ordered on one stream.
+// The scratch registered with det_gemm_set_scratch (the reference's per-(token, group) activation-sum buffer,
+// gemm.cu:913-936).  This backend's kernels need no caller scratch: the pointer is kept for the ABI only.
 void* g_user_scratch = nullptr;
 size_t g_user_scratch_bytes = 0;
-int* g_cinit = nullptr;
-size_t g_cinit_cap = 0;             // elements
-
-int* cinit_scratch(int M, int G, hipStream_t st) {
-    const size_t need = (size_t)M * G;
-    if (g_user_scratch && need * sizeof(int) <= g_user_scratch_bytes) return (int*)g_user_scratch;
-    static bool noted = false;
-    if (!noted) {
-        fprintf(stderr, "det_gemm: note: no scratch (or too small, have %zu bytes, need %zu for M=%d K=%d) set with "
-                        "det_gemm_set_scratch; using a lazily allocated global buffer\n",
-                g_user_scratch_bytes, need * sizeof(int), M, G * GROUP);
-        noted = true;
-    }
-    if (need > g_cinit_cap) {
-        DET_CHECK(hipStreamSynchronize(st));     // earlier launches may still use the old buffer
-        if (g_cinit) DET_CHECK(hipFree(g_cinit));
-        g_cinit_cap = std::max(need, (size_t)4096 * 136);
-        DET_CHECK(hipMalloc(&g_cinit, g_cinit_cap * sizeof(int)));
-    }
-    return g_cinit;
-}
 
 // K-split buffers of k_decode: int64 accumulators part[MP][Npad] and per-tile arrival counters, zero between calls
 // (the last workgroup of each tile clears what it used); library-owned, grown on demand.  Calls that overlap on
@@ -1104,14 +1048,7 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         launch_mfma<BITS, 64>(L, xq, sx, mx, M, y, st);
     } else {
         const int nbn = (L.N + PF_BN - 1) / PF_BN, nbt = (M + PF_BM - 1) / PF_BM;
-        int* ci = nullptr;
-        if (BITS != 8) {
-            const int G = L.K / GROUP;
-            ci = cinit_scratch(M, G, st);
-            k_cinit<<<(M * G + 255) / 256, 256, 0, st>>>(xq, M * G, BITS == 6 ? 32 : 8, ci);
-            DET_CHECK(hipGetLastError());
-        }
-        k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, ci, M, y, nbn, nbt);
+        k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
         DET_CHECK(hipGetLastError());
     }
 }
