@@ -73,10 +73,9 @@ void det_silu_mul_quant(const float* g, const float* u, int M, int n, float* h, 
 void det_gemm(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, hipStream_t st);
 void det_gemm_ex(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, int accumulate,
                  int nparts, const int* offs, float* const* dsts, hipStream_t st);
-// Scratch for the W4/W6 M > 64 path (per-(token, 128-group) activation sums), same contract as det_cuda.h:52-57:
-// a device buffer of at least det_gemm_scratch_bytes(M, K) bytes for the largest M and K in use, set once with
-// det_gemm_set_scratch (the host keeps it alive; NULL unsets).  Without one (or with a too small one) a lazily
-// allocated global buffer is used instead (one-time note on stderr).
+// Scratch contract of det_cuda.h:52-57 (there: per-(token, 128-group) activation sums for W4/W6 with M > 64):
+// det_gemm_scratch_bytes(M, K) returns the same size, and det_gemm_set_scratch registers a host-owned buffer (NULL
+// unsets).  This backend's kernels need no caller scratch, so the buffer is accepted and left unused.
 size_t det_gemm_scratch_bytes(int M, int K);
 void det_gemm_set_scratch(void* p, size_t bytes);
 
