@@ -121,6 +121,66 @@ __device__ __forceinline__ void mac_s32_u32(long long& acc, int p, uint32_t s) {
     acc = (long long)r;
 }
 
+// ------------------------------------------------------------------ global -> LDS copies
+// Global -> LDS copy by the buffer unit (BYTES = 4 or 16 per lane, lane i's bytes land at lds + i * BYTES), written as
+// inline assembly so that the compiler does not track it: with the builtin it cannot tell that later LDS reads touch
+// other buffers and waits for every copy in flight before the first of them.  The caller waits (s_waitcnt vmcnt)
+// and synchronises before reading the target.  `lds` must be wave-uniform.
+template <int BYTES>
+__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff_, const void* lds) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
+    if (BYTES == 16)
+        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
+}
+
+// N (<= 4) copies of 16 bytes per lane under one M0 value: copy i reads the resource at voff[i] + soff + 1024 i and
+// lands at lds + 1024 i + 16 lane (the instruction offset moves both addresses).  Changing M0 stalls until the copies
+// issued before have consumed it, so each run sets it once.
+template <int N>
+__device__ __forceinline__ void dma16_run(__amdgpu_buffer_rsrc_t r, const uint32_t* voff, uint32_t soff_, const void* lds) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);      // uniform by construction; keep it scalar
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
+    static_assert(N >= 1 && N <= 4, "at most 4 copies per run");
+    if constexpr (N == 4)
+        asm volatile("s_mov_b32 m0, %5\n\t"
+                     "buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
+                     "buffer_load_dwordx4 %1, %4, %6 offen offset:1024 lds\n\t"
+                     "buffer_load_dwordx4 %2, %4, %6 offen offset:2048 lds\n\t"
+                     "buffer_load_dwordx4 %3, %4, %6 offen offset:3072 lds"
+                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+    else if constexpr (N == 3)
+        asm volatile("s_mov_b32 m0, %4\n\t"
+                     "buffer_load_dwordx4 %0, %3, %5 offen lds\n\t"
+                     "buffer_load_dwordx4 %1, %3, %5 offen offset:1024 lds\n\t"
+                     "buffer_load_dwordx4 %2, %3, %5 offen offset:2048 lds"
+                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+    else if constexpr (N == 2)
+        asm volatile("s_mov_b32 m0, %3\n\t"
+                     "buffer_load_dwordx4 %0, %2, %4 offen lds\n\t"
+                     "buffer_load_dwordx4 %1, %2, %4 offen offset:1024 lds"
+                     :: "v"(voff[0]), "v"(voff[1]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\t"
+                     "buffer_load_dwordx4 %0, %1, %3 offen lds"
+                     :: "v"(voff[0]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+}
+// four copies under one M0, copy i through resource r[i] at voff[i % 2] + soff + 1024 i, landing at
+// lds + 1024 i + 16 lane
+__device__ __forceinline__ void dma16_run4x(const __amdgpu_buffer_rsrc_t* r, uint32_t voff0, uint32_t voff1, uint32_t soff_,
+                                            const void* lds) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %6\n\t"
+                 "buffer_load_dwordx4 %0, %2, %7 offen lds\n\t"
+                 "buffer_load_dwordx4 %1, %3, %7 offen offset:1024 lds\n\t"
+                 "buffer_load_dwordx4 %0, %4, %7 offen offset:2048 lds\n\t"
+                 "buffer_load_dwordx4 %1, %5, %7 offen offset:3072 lds"
+                 :: "v"(voff0), "v"(voff1), "s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[3]), "s"(m0v), "s"(soff) : "memory", "m0");
+}
+
 // ------------------------------------------------------------------ decode (M <= 16)
 // Grid: T tiles x KS K-slices, one workgroup each, S waves per workgroup; wave w of slice k takes the groups
 // g0(k) + w, g0(k) + w + S, ... (normally exactly one), issuing all its loads before any arithmetic.  The waves'
@@ -308,6 +368,151 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
     }
 }
 
+// ------------------------------------------------------------------ decode, several token sets (16 < M <= 64)
+// k_decode's matrix-core form over several sets of 16 tokens.  A wave owns NSW sets (its token part, one of TP) and
+// walks the groups g0 + slot, g0 + slot + S, ... of its tile: per group it unpacks its 64 rows once and runs 8 MFMAs
+// per set (the A operand of a set laid out as for MP = 16).  Software pipeline: the next group's weight words are
+// loaded into registers and its activations (the wave's 16 NSW token rows) copied into the wave's other LDS area
+// before the current group is computed, so a group costs compute, not a memory round trip.  The waves of a tile's
+// token parts read the same weight lines (the second read comes from L2).  At the end the waves add their int64
+// sums into one LDS accumulator with ds_add_u64; K-slices across workgroups combine as in k_decode.
+template <int BITS, int NSW, int TP>
+__global__ void __launch_bounds__(512) k_decode_ms(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
+                                                   const uint16_t* __restrict__ ms, int N, int K,
+                                                   const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                   const uint16_t* __restrict__ mx, int M, Out out, int KS,
+                                                   long long* __restrict__ part, unsigned int* __restrict__ cnt) {
+    constexpr int NC = group_bytes(BITS) / 16;
+    constexpr int MP = 16 * NSW * TP;           // tokens per launch
+    constexpr int XB = 16 * NSW * 128;          // bytes of one activation area (16 NSW rows of 128 bytes)
+    __shared__ long long tot_s[MP * 64];        // [set * 16 + register][lane] int64 sums of the workgroup
+    extern __shared__ __attribute__((aligned(16))) int8_t xs_dyn[];   // [wave][2 areas][16 NSW rows][128 bytes]
+    __shared__ unsigned int last_s;
+    __shared__ __attribute__((aligned(16))) uint32_t mxs_s[16][16 * NSW];   // each wave's token multipliers
+    const int lane = threadIdx.x & 63, W = blockDim.x >> 6, S = W / TP;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tp = wv % TP, slot = wv / TP;      // token part and group slot of this wave
+    const int tile = blockIdx.x / KS, ks = blockIdx.x - tile * KS;
+    const int G = K / GROUP;
+    const int gs = (G + KS - 1) / KS;
+    const int g0 = ks * gs, g1 = min(G, g0 + gs);
+    for (int e = threadIdx.x; e < MP * 64; e += blockDim.x) tot_s[e] = 0;
+    long long acc[NSW][16];
+#pragma unroll
+    for (int t = 0; t < NSW; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0;
+    int8_t* xa0 = xs_dyn + wv * 2 * XB;
+    int8_t* xa1 = xa0 + XB;
+    const int tbase = tp * 16 * NSW;            // first token of this wave's part
+    // activation copy c of a group: rows 8 c + lane / 8 of the part; LDS slot lane % 8 of row R holds chunk
+    // (lane % 8) ^ ((R / 2) % 8); rows past M read as zero (range check on the per-lane offset)
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, M * K, 0x00020000);
+    uint32_t xvo[2 * NSW];
+#pragma unroll
+    for (int c = 0; c < 2 * NSW; c++) {
+        const int R = 8 * c + (lane >> 3);
+        xvo[c] = (uint32_t)((tbase + R) * K + (((lane & 7) ^ ((R >> 1) & 7)) * 16)) - 1024u * (c & 3);
+    }
+    const int ai = lane & 31;
+    const int aoff = (lane < 32) ? (ai < 16 ? ai : -1) : (ai >= 16 ? ai - 16 : -1);   // token within a set (-1: none)
+
+    // loads of group g: activations into area xd (one run per 4 KB), weight words into q, the tile's two row
+    // multipliers and (lane t) token tbase + t's multiplier into mlo_n / mhi_n / mxl_n
+    uint32_t q[NC * 4];
+    uint32_t mlo_n = 0, mhi_n = 0, mxl_n = 0;
+    auto fetch = [&](int g, int8_t* xd) {
+#pragma unroll
+        for (int c0 = 0; c0 < 2 * NSW; c0 += 4) {
+            if (2 * NSW - c0 >= 4) dma16_run<4>(xr, xvo + c0, g * GROUP, xd + c0 * 1024);
+            else dma16_run<2>(xr, xvo + c0, g * GROUP, xd + c0 * 1024);
+        }
+        const v4i* src = reinterpret_cast<const v4i*>(wq + ((size_t)tile * G + g) * NC * 1024) + lane;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const v4i v = __builtin_nontemporal_load(src + c * 64);
+            q[4 * c] = v.x; q[4 * c + 1] = v.y; q[4 * c + 2] = v.z; q[4 * c + 3] = v.w;
+        }
+        const size_t tg = (size_t)tile * G + g;
+        mlo_n = ms[tg * 64 + (lane & 31)];
+        mhi_n = ms[tg * 64 + (lane & 31) + 32];
+        const int tl = tbase + lane;                              // lane t: token tbase + t
+        mxl_n = lane < 16 * NSW && tl < M ? (mx ? (uint32_t)mx[(size_t)tl * G + g] : 1u) : 0u;
+    };
+    auto compute = [&](const int8_t* xd, const uint32_t* w, uint32_t mlo, uint32_t mhi, uint32_t mxl) {
+        uint32_t* mxw = mxs_s[wv];
+        if (lane < 16 * NSW) mxw[lane] = mxl;                   // read back below by this wave only (in order)
+#pragma unroll
+        for (int t = 0; t < NSW; t++) {
+            const int R = 16 * t + max(aoff, 0);                  // this lane's A row (token) within the part
+            v16i d = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const v4i z = {0, 0, 0, 0};
+                const v4i xa = aoff >= 0 ? *reinterpret_cast<const v4i*>(xd + R * 128 + ((c ^ ((R >> 1) & 7)) << 4)) : z;
+                const v4i bw = {(int)w[4 * c], (int)w[4 * c + 1], (int)w[4 * c + 2], (int)w[4 * c + 3]};
+                d = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, bw, d, 0, 0, 0);
+            }
+            // register r = 4 q + e: A row i = 8 q + e (low half of the wave) or 8 q + 4 + e (high half); i < 16 is token
+            // i of row lane % 32, i >= 16 token i - 16 of row lane % 32 + 32.  So the four registers of q take four
+            // consecutive tokens from (8 q + 4 (lane / 32)) % 16, and row multiplier mlo (q < 2) or mhi (q >= 2).
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                const uint4 mv = *reinterpret_cast<const uint4*>(mxw + 16 * t + ((8 * qq + 4 * (lane >> 5)) & 15));
+                const uint32_t mxv[4] = {mv.x, mv.y, mv.z, mv.w};
+                const uint32_t mrow = qq >= 2 ? mhi : mlo;
+#pragma unroll
+                for (int e = 0; e < 4; e++) mac_s32_u32(acc[t][4 * qq + e], d[4 * qq + e], mrow * mxv[e]);
+            }
+        }
+    };
+
+    int g = g0 + slot;
+    if (g < g1) fetch(g, xa0);
+    for (int par = 0; g < g1; g += S, par ^= 1) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // group g's copies and loads have landed
+        uint32_t w[32];
+#pragma unroll
+        for (int b = 0; b < 4; b++) block_signed<BITS>(q + b * NC, w + 8 * b);
+        const uint32_t mlo = mlo_n, mhi = mhi_n, mxl = mxl_n;
+        const int8_t* xd = par ? xa1 : xa0;
+        if (g + S < g1) fetch(g + S, par ? xa0 : xa1);        // the next group's loads run under this compute
+        compute(xd, w, mlo, mhi, mxl);
+    }
+#pragma unroll
+    for (int t = 0; t < NSW; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (g0 + slot < g1)
+                __hip_atomic_fetch_add(tot_s + ((tp * NSW + t) * 16 + r) * 64 + lane, acc[t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __syncthreads();
+    // thread (wave w, lane) finishes registers R = w, w + W, ... of the sums
+    const size_t npad = (size_t)(gridDim.x / KS) * TILE_N;
+    if (KS > 1) {
+        for (int R = wv; R < MP; R += W) {
+            const int t = 16 * (R >> 4) + dec_tok<16>(R & 15, lane), n = tile * TILE_N + dec_row<16>(R & 15, lane);
+            if (t < M) __hip_atomic_fetch_add(part + (size_t)t * npad + n, tot_s[R * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);             // this wave's adds have been performed
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);
+        __syncthreads();
+        if (!last_s) return;
+        for (int R = wv; R < MP; R += W) {
+            const int t = 16 * (R >> 4) + dec_tok<16>(R & 15, lane), n = tile * TILE_N + dec_row<16>(R & 15, lane);
+            const long long v = t < M ? __hip_atomic_exchange(part + (size_t)t * npad + n, 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+            if (t < M && n < N) out.store(N, t, n, (i64_to_f(v) * cs[n]) * sx[t]);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    for (int R = wv; R < MP; R += W) {
+        const int t = 16 * (R >> 4) + dec_tok<16>(R & 15, lane), n = tile * TILE_N + dec_row<16>(R & 15, lane);
+        if (t < M && n < N) out.store(N, t, n, (i64_to_f(tot_s[R * 64 + lane]) * cs[n]) * sx[t]);
+    }
+}
+
 // ------------------------------------------------------------------ MFMA GEMM (16 < M <= 64)
 constexpr int MF_BN = 128;          // output rows n per workgroup (two 64-row tiles)
 constexpr int MF_STR = 144;         // LDS row stride in bytes (128 codes + 16 pad)
@@ -453,64 +658,6 @@ __device__ __forceinline__ void digits16(uint32_t v, int& d1, int& d0) {
 // (chunk position c ^ ((r / 2) % 8): the 16 rows that one LDS cycle serves fall on 16 distinct 16-byte bank slots)
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
-// Global -> LDS copy by the buffer unit (BYTES = 4 or 16 per lane, lane i's bytes land at lds + i * BYTES), written as
-// inline assembly so that the compiler does not track it: with the builtin it cannot tell that later LDS reads touch
-// other buffers and waits for every copy in flight before the first of them.  The caller waits (s_waitcnt vmcnt)
-// and synchronises before reading the target.  `lds` must be wave-uniform.
-template <int BYTES>
-__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff_, const void* lds) {
-    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    if (BYTES == 16)
-        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
-    else
-        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
-}
-
-// N (<= 4) copies of 16 bytes per lane under one M0 value: copy i reads the resource at voff[i] + soff + 1024 i and
-// lands at lds + 1024 i + 16 lane (the instruction offset moves both addresses).  Changing M0 stalls until the copies
-// issued before have consumed it, so each run sets it once.
-template <int N>
-__device__ __forceinline__ void dma16_run(__amdgpu_buffer_rsrc_t r, const uint32_t* voff, uint32_t soff_, const void* lds) {
-    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);      // uniform by construction; keep it scalar
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    static_assert(N >= 1 && N <= 4, "at most 4 copies per run");
-    if constexpr (N == 4)
-        asm volatile("s_mov_b32 m0, %5\n\t"
-                     "buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
-                     "buffer_load_dwordx4 %1, %4, %6 offen offset:1024 lds\n\t"
-                     "buffer_load_dwordx4 %2, %4, %6 offen offset:2048 lds\n\t"
-                     "buffer_load_dwordx4 %3, %4, %6 offen offset:3072 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-    else if constexpr (N == 3)
-        asm volatile("s_mov_b32 m0, %4\n\t"
-                     "buffer_load_dwordx4 %0, %3, %5 offen lds\n\t"
-                     "buffer_load_dwordx4 %1, %3, %5 offen offset:1024 lds\n\t"
-                     "buffer_load_dwordx4 %2, %3, %5 offen offset:2048 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-    else if constexpr (N == 2)
-        asm volatile("s_mov_b32 m0, %3\n\t"
-                     "buffer_load_dwordx4 %0, %2, %4 offen lds\n\t"
-                     "buffer_load_dwordx4 %1, %2, %4 offen offset:1024 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-    else
-        asm volatile("s_mov_b32 m0, %2\n\t"
-                     "buffer_load_dwordx4 %0, %1, %3 offen lds"
-                     :: "v"(voff[0]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-}
-// four copies under one M0, copy i through resource r[i] at voff[i % 2] + soff + 1024 i, landing at
-// lds + 1024 i + 16 lane
-__device__ __forceinline__ void dma16_run4x(const __amdgpu_buffer_rsrc_t* r, uint32_t voff0, uint32_t voff1, uint32_t soff_,
-                                            const void* lds) {
-    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    asm volatile("s_mov_b32 m0, %6\n\t"
-                 "buffer_load_dwordx4 %0, %2, %7 offen lds\n\t"
-                 "buffer_load_dwordx4 %1, %3, %7 offen offset:1024 lds\n\t"
-                 "buffer_load_dwordx4 %0, %4, %7 offen offset:2048 lds\n\t"
-                 "buffer_load_dwordx4 %1, %5, %7 offen offset:3072 lds"
-                 :: "v"(voff0), "v"(voff1), "s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[3]), "s"(m0v), "s"(soff) : "memory", "m0");
-}
 
 #ifdef PF_TRACE
 __device__ unsigned long long g_trace[4 * 64 * 8];
@@ -1030,6 +1177,30 @@ void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, cons
     DET_CHECK(hipGetLastError());
 }
 
+template <int BITS, int NSW, int TP>
+void launch_decode_ms(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
+    const int G = L.K / GROUP;
+    const int T = (L.N + TILE_N - 1) / TILE_N;
+    const int cus = g_decode_waves / 8;
+    int KS = 1;
+    if (2 * T < cus) KS = std::max(1, std::min((cus + T - 1) / T, (G + 3) / 4));
+    const int gs = (G + KS - 1) / KS;
+    // group slots per workgroup: enough waves for the device, each slot walking at least two groups so that the
+    // pipeline has something to overlap
+    int S = (g_decode_waves + T * KS * TP - 1) / (T * KS * TP);
+    S = std::max(1, std::min(S, std::min((gs + 1) / 2, 8 / TP)));
+    long long* part = nullptr;
+    unsigned int* cnt = nullptr;
+    if (KS > 1) {
+        decode_buffers((size_t)16 * NSW * TP * T * TILE_N, (size_t)T, st);
+        part = g_part;
+        cnt = g_cnt;
+    }
+    const size_t lds = (size_t)S * TP * 2 * 16 * NSW * 128;         // two activation areas per wave
+    k_decode_ms<BITS, NSW, TP><<<T * KS, 64 * S * TP, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
+    DET_CHECK(hipGetLastError());
+}
+
 template <int BITS, int BM>
 void launch_mfma(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
     dim3 grid((L.N + MF_BN - 1) / MF_BN, (M + BM - 1) / BM);
@@ -1045,7 +1216,8 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         else if (M <= 8) launch_decode<BITS, 8>(L, xq, sx, mx, M, y, st);
         else launch_decode<BITS, 16>(L, xq, sx, mx, M, y, st);
     } else if (M <= 64) {
-        launch_mfma<BITS, 64>(L, xq, sx, mx, M, y, st);
+        if (M <= 32) launch_decode_ms<BITS, 2, 1>(L, xq, sx, mx, M, y, st);
+        else launch_decode_ms<BITS, 2, 2>(L, xq, sx, mx, M, y, st);
     } else {
         const int nbn = (L.N + PF_BN - 1) / PF_BN, nbt = (M + PF_BM - 1) / PF_BM;
         k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);

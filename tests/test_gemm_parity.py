@@ -198,14 +198,15 @@ def test_baseline_w6_9728x2560(M):
 
 @pytest.mark.parametrize('bits', [8, 6, 4])
 def test_decode_every_m(bits):
-    """Every small batch M = 1..17 (each decode variant: dot-product M = 1, matrix-core M = 2..16, tiled 17), on a
+    """Every small batch M = 1..65 (each decode variant: dot-product M = 1, matrix-core M = 2..16, two to four token
+    sets M = 17..64, tiled M = 65), on a
     shape whose tiles are few (split over K, int64 atomics across workgroups) and one whose tiles fill the device;
     group and per-row activation scales; repeated calls, so the split's accumulators must come back to zero."""
     rng = oracle.Rng(300 + bits)
     for n, k in ((200, 3072), (9000, 512)):
         rows = rng.fake_rows(bits, n, k)
         lin = ffi.Linear(rows, k, bits)
-        for m in range(1, 18):
+        for m in range(1, 66):
             x = rng.acts_x(m, k)
             for group in (True, False):
                 print(f'decode W{bits} n={n} k={k} m={m} group={group}', flush=True)
