@@ -49,25 +49,18 @@ __device__ __forceinline__ int clamp_i8(float v) {
     return (int)v;
 }
 
-// int64 -> fp32 with round-to-nearest-even, written out from the definition: keep the 24 leading significant
-// bits, round on the dropped bits (above half, or exactly half with an odd kept part, rounds up).
-__device__ __forceinline__ float i64_to_f(long long v) {
+// int64 -> fp32 with round-to-nearest-even: shift the magnitude so that its leading one is bit 63, fold the low
+// 32 bits into a sticky bit 0 of the high word, and let the hardware's u32 -> f32 conversion (round to nearest
+// even) round that word; the sticky bit lies below the rounding position, so it only breaks exact ties, as the
+// dropped bits would.  ldexp then restores the scale exactly.
+__host__ __device__ __forceinline__ float i64_to_f(long long v) {
     const unsigned long long a = v < 0 ? 0ull - (unsigned long long)v : (unsigned long long)v;
     if (a == 0) return 0.0f;
-    const int e = 63 - __builtin_clzll(a);            // position of the leading one
-    unsigned int mant;                                 // 24-bit significand with the leading one, may carry to 2^24
-    if (e <= 23) {
-        mant = (unsigned int)(a << (23 - e));
-    } else {
-        const int sh = e - 23;
-        const unsigned long long kept = a >> sh;
-        const unsigned long long rem = a & ((1ull << sh) - 1);
-        const unsigned long long half = 1ull << (sh - 1);
-        mant = (unsigned int)kept + ((rem > half || (rem == half && (kept & 1))) ? 1u : 0u);
-    }
-    // (e + 127 - 1) << 23 plus the significand: a carry out of 24 bits bumps the exponent by itself
-    const unsigned int bits = ((unsigned int)(e + 126) << 23) + mant;
-    return __uint_as_float(bits | (v < 0 ? 0x80000000u : 0u));
+    const int lz = __builtin_clzll(a);
+    const unsigned long long nrm = a << lz;
+    const unsigned int hi = (unsigned int)(nrm >> 32) | ((unsigned int)nrm != 0u ? 1u : 0u);
+    const float f = __builtin_ldexpf((float)hi, 32 - lz);
+    return v < 0 ? -f : f;
 }
 
 // ---- spec/prim.rs:78-149 transcendental op sequences (Cephes-derived, explicit fp32 ops; no libm).

@@ -14,9 +14,11 @@
 //       registers.  M == 1: dots with the activations (scalar loads) by v_dot4c_i32_i8; 2 <= M <= 16: one
 //       v_mfma_i32_32x32x32_i8 per 16 k-bytes carries the 64 rows x MP tokens.  The int32 group partial is scaled by
 //       m*mx into int64; the waves of a workgroup add in LDS, the K-slices of a tile by int64 atomics.
-//   k_mfma<BITS,BM> (16 < M <= 64): 128-row x BM-token workgroup tile, 4 waves of (BM/2) x 64.  Per 128-group the
-//       activation tile and the unpacked (signed int8) weight tile are staged in LDS; v_mfma_i32_32x32x32_i8 gives
-//       the exact int32 group partials, which are scaled into int64 accumulators before the next group.
+//   k_decode_ms<BITS,TS> (16 < M <= 64): 64-row tiles x K-slices; a wave owns 32 rows x all MT = 32 TS tokens,
+//       each lane half a row's packed group (no duplicate loads or unpacking); the activations come global -> LDS by
+//       the buffer unit; one v_mfma_i32_32x32x32_i8 per 32 codes and token set; group scaling with two VALU ops per
+//       output (biased partials, bias removed by digit-product MFMAs once per workgroup).
+//   k_prefill<BITS> (M > 64): 128 x 128 workgroup tiles, LDS double buffering, the same biased scaling.
 #include <string.h>
 #include <algorithm>
 #include "common.h"
@@ -368,262 +370,298 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
     }
 }
 
-// ------------------------------------------------------------------ decode, several token sets (16 < M <= 64)
-// k_decode's matrix-core form over several sets of 16 tokens.  A wave owns NSW sets (its token part, one of TP) and
-// walks the groups g0 + slot, g0 + slot + S, ... of its tile: per group it unpacks its 64 rows once and runs 8 MFMAs
-// per set (the A operand of a set laid out as for MP = 16).  Software pipeline: the next group's weight words are
-// loaded into registers and its activations (the wave's 16 NSW token rows) copied into the wave's other LDS area
-// before the current group is computed, so a group costs compute, not a memory round trip.  The waves of a tile's
-// token parts read the same weight lines (the second read comes from L2).  At the end the waves add their int64
-// sums into one LDS accumulator with ds_add_u64; K-slices across workgroups combine as in k_decode.
-template <int BITS, int NSW, int TP>
-__global__ void __launch_bounds__(512) k_decode_ms(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
-                                                   const uint16_t* __restrict__ ms, int N, int K,
-                                                   const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                   const uint16_t* __restrict__ mx, int M, Out out, int KS,
-                                                   long long* __restrict__ part, unsigned int* __restrict__ cnt) {
-    constexpr int NC = group_bytes(BITS) / 16;
-    constexpr int MP = 16 * NSW * TP;           // tokens per launch
-    constexpr int XB = 16 * NSW * 128;          // bytes of one activation area (16 NSW rows of 128 bytes)
-    __shared__ long long tot_s[MP * 64];        // [set * 16 + register][lane] int64 sums of the workgroup
-    extern __shared__ __attribute__((aligned(16))) int8_t xs_dyn[];   // [wave][2 areas][16 NSW rows][128 bytes]
+// balanced digits of a 16-bit multiplier: v = 256 d1 + d0 + 32896 with d1, d0 in [-128, 127]
+constexpr uint32_t PF_BIAS = 1u << 21;
+constexpr int DIG_C = 32896;
+
+__device__ __forceinline__ void digits16(uint32_t v, int& d1, int& d0) {
+    const int vp = (int)v - DIG_C;
+    d0 = ((vp + 128) & 255) - 128;
+    d1 = (vp - d0) >> 8;
+}
+// ------------------------------------------------------------------ decode, many tokens (16 < M <= 64)
+// A workgroup of P (<= 4) wave pairs walks the groups g0 .. g1-1 of one tile's K-slice, pair p taking groups
+// g0 + p, g0 + p + P, ... (one round = one group per pair); wave h of a pair owns weight rows 32 h .. 32 h + 31 of the
+// tile for all MT = 32 TS tokens.  Lane l holds row 32 h + l % 32 and k-half e = l / 32 of the group: packed blocks
+// 2 e and 2 e + 1 (whole chunk planes in every format), so no lane loads or unpacks what another lane does.  Per 32
+// k-codes step s (0..3) the lane's B operand is its codes 64 e + 16 s .. + 15 and the A operand of lane l the same
+// codes of token l % 32 (+ 32 ts), so one v_mfma_i32_32x32x32_i8 per step and token set gives the 32 x 32 (token,
+// row) group partials in the standard layout: lane l keeps row 32 h + l % 32, register r token 8 (r / 4) + 4 e + r % 4.
+// Scaling as in k_prefill: each chain starts from B = 2^21 and U += (p + B) * (m * mx) (one v_mul_u32_u24, one
+// v_mad_u64_u32).  B * S, S = sum_g m * mx, is removed once per workgroup: every round stages the 7-bit digits of its
+// group's m (per row) and mx (per token) in LDS at the group's slot, and after the loop 9 digit-product MFMAs per 32
+// slots give S for each 32 x 32 block exactly.
+// The activations of a pair's group (MT rows of 128 bytes, chunk-swizzled) are copied global -> LDS by the buffer
+// unit, half by each wave; the workgroup runs in lockstep (one barrier per round) with the next round's weight words
+// and activations in flight while the current round computes (two LDS areas).  With P = 2 two workgroups share a CU,
+// so one's prologue and epilogue overlap the other's rounds.  The waves' int64 sums meet in LDS (over the activation areas);
+// with KS > 1 every slice stores its sums (agent-scope stores, coherent across the XCDs' L2s) into its own plane of
+// `part`, counts itself in cnt[tile], and the last slice to arrive adds the other planes and writes the outputs.
+constexpr int DMS_MAXP = 4;          // wave pairs per workgroup
+constexpr int DMS_MAXSLOT = 96;      // groups per K-slice (digit slots in LDS)
+#if defined(PF_TRACE) || defined(DMS_TRACE)
+__device__ unsigned long long g_trace[4 * 64 * 8];
+#endif
+#ifdef DMS_TRACE
+#define DMS_TR(h, slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
+    __builtin_amdgcn_sched_barrier(0); if (blockIdx.x < 4 && threadIdx.x == 0 && (h) < 64) g_trace[(blockIdx.x * 64 + (h)) * 8 + (slot)] = tr_; } while (0)
+#else
+#define DMS_TR(h, slot) do {} while (0)
+#endif
+__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {   // exact for a, b < 2^24 with a * b < 2^32
+    uint32_t r;
+    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// bytes of v (slots s0 .. s0 + 3) at or past slot n set to zero
+__device__ __forceinline__ int mask_slots(int v, int s0, int n) {
+    const int k = n - s0;
+    return k >= 4 ? v : k <= 0 ? 0 : (int)((uint32_t)v & (0xffffffffu >> (32 - 8 * k)));
+}
+template <int BITS, int TS>
+__global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
+                                                                const uint16_t* __restrict__ ms, int N, int K,
+                                                                const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                                const uint16_t* __restrict__ mx, int M, Out out, int KS,
+                                                                long long* __restrict__ part, unsigned int* __restrict__ cnt) {
+    constexpr int NC = group_bytes(BITS) / 16;  // chunk planes per row-group; a k-half is NC / 2 of them
+    constexpr int NH = NC / 2;
+    constexpr int MT = 32 * TS;                 // tokens per launch
+    constexpr int XB = MT * 128;                // bytes of one group's activations
+    constexpr int NCP = MT / 16;                // 1 KB copies per wave per group (half the rows)
+    // dynamic LDS: [2 areas][P pairs][MT rows][128] activations (later the int64 sums [MT][64]), then the digits
+    // [3][64 rows][NS] of m and [3][MT][NS] of mx (NS = slots, a multiple of 32)
+    extern __shared__ __attribute__((aligned(16))) int8_t xs_dyn[];
+    __shared__ __attribute__((aligned(16))) uint32_t mxs_s[2 * DMS_MAXP][MT];   // each wave's token multipliers
+    __shared__ float sxs_s[MT];
     __shared__ unsigned int last_s;
-    __shared__ __attribute__((aligned(16))) uint32_t mxs_s[16][16 * NSW];   // each wave's token multipliers
-    const int lane = threadIdx.x & 63, W = blockDim.x >> 6, S = W / TP;
+    const int lane = threadIdx.x & 63, W = blockDim.x >> 6, P = W >> 1;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tp = wv % TP, slot = wv / TP;      // token part and group slot of this wave
+    const int pr = wv >> 1, hf = wv & 1;        // pair and row half of this wave
+    const int e = lane >> 5, l32 = lane & 31, row = 32 * hf + l32;
     const int tile = blockIdx.x / KS, ks = blockIdx.x - tile * KS;
     const int G = K / GROUP;
     const int gs = (G + KS - 1) / KS;
-    const int g0 = ks * gs, g1 = min(G, g0 + gs);
-    for (int e = threadIdx.x; e < MP * 64; e += blockDim.x) tot_s[e] = 0;
-    long long acc[NSW][16];
+    const int g0 = ks * gs, g1 = min(G, g0 + gs), ng = g1 - g0;
+    const int NS = (gs + 31) & ~31;
+    const int rounds = (gs + P - 1) / P;        // the same for every wave: each round ends at a barrier
+    const int n = tile * TILE_N + lane;         // output row of this thread in the epilogue
+    // epilogue operands, loaded now so that their latency hides under the rounds
+    const float cn = n < N ? cs[n] : 0.0f;
+    const float sxl = wv == 0 && lane < MT ? sx[min(lane, M - 1)] : 0.0f;
+    unsigned long long U[TS][16];
 #pragma unroll
-    for (int t = 0; t < NSW; t++)
+    for (int t = 0; t < TS; t++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) acc[t][r] = 0;
-    int8_t* xa0 = xs_dyn + wv * 2 * XB;
-    int8_t* xa1 = xa0 + XB;
-    const int tbase = tp * 16 * NSW;            // first token of this wave's part
-    // activation copy c of a group: rows 8 c + lane / 8 of the part; LDS slot lane % 8 of row R holds chunk
-    // (lane % 8) ^ ((R / 2) % 8); rows past M read as zero (range check on the per-lane offset)
+        for (int r = 0; r < 16; r++) U[t][r] = 0;
+    const int tot_bytes = max(2 * P * XB, MT * TILE_N * 8);
+    int8_t* wdig = xs_dyn + tot_bytes;           // [3][64][NS]
+    int8_t* xdig = wdig + 3 * 64 * NS;           // [3][MT][NS]
+    // activation copy c of this wave: row R = MT/2 hf + 8 c + lane / 8; LDS slot lane % 8 of row R holds chunk
+    // (lane % 8) ^ ((R / 2) % 8).  Rows past M lie beyond the resource's range and read as zero.
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, M * K, 0x00020000);
-    uint32_t xvo[2 * NSW];
+    uint32_t xvo[NCP];
 #pragma unroll
-    for (int c = 0; c < 2 * NSW; c++) {
-        const int R = 8 * c + (lane >> 3);
-        xvo[c] = (uint32_t)((tbase + R) * K + (((lane & 7) ^ ((R >> 1) & 7)) * 16)) - 1024u * (c & 3);
+    for (int c = 0; c < NCP; c++) {
+        const int R = (MT / 2) * hf + 8 * c + (lane >> 3);
+        xvo[c] = (uint32_t)(R * K + (((lane & 7) ^ ((R >> 1) & 7)) * 16)) - 1024u * (c & 3);
     }
-    const int ai = lane & 31;
-    const int aoff = (lane < 32) ? (ai < 16 ? ai : -1) : (ai >= 16 ? ai - 16 : -1);   // token within a set (-1: none)
+    auto area = [&](int par) __attribute__((always_inline)) { return xs_dyn + (par * P + pr) * XB; };
 
-    // loads of group g: activations into area xd (one run per 4 KB), weight words into q, the tile's two row
-    // multipliers and (lane t) token tbase + t's multiplier into mlo_n / mhi_n / mxl_n
-    uint32_t q[NC * 4];
-    uint32_t mlo_n = 0, mhi_n = 0, mxl_n = 0;
-    auto fetch = [&](int g, int8_t* xd) {
+    uint32_t q[NH * 4];
+    uint32_t m_n = 0, mxl_n = 0;
+    auto fetch = [&](int g, int8_t* xd) __attribute__((always_inline)) {
 #pragma unroll
-        for (int c0 = 0; c0 < 2 * NSW; c0 += 4) {
-            if (2 * NSW - c0 >= 4) dma16_run<4>(xr, xvo + c0, g * GROUP, xd + c0 * 1024);
-            else dma16_run<2>(xr, xvo + c0, g * GROUP, xd + c0 * 1024);
+        for (int c0 = 0; c0 < NCP; c0 += 4) {
+            if (NCP - c0 >= 4) dma16_run<4>(xr, xvo + c0, g * GROUP, xd + (MT / 2) * hf * 128 + c0 * 1024);
+            else dma16_run<2>(xr, xvo + c0, g * GROUP, xd + (MT / 2) * hf * 128 + c0 * 1024);
         }
-        const v4i* src = reinterpret_cast<const v4i*>(wq + ((size_t)tile * G + g) * NC * 1024) + lane;
+        const size_t tg = (size_t)tile * G + g;
+        const v4i* src = reinterpret_cast<const v4i*>(wq + tg * NC * 1024 + (size_t)NH * e * 1024) + row;
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
+        for (int c = 0; c < NH; c++) {
             const v4i v = __builtin_nontemporal_load(src + c * 64);
             q[4 * c] = v.x; q[4 * c + 1] = v.y; q[4 * c + 2] = v.z; q[4 * c + 3] = v.w;
         }
-        const size_t tg = (size_t)tile * G + g;
-        mlo_n = ms[tg * 64 + (lane & 31)];
-        mhi_n = ms[tg * 64 + (lane & 31) + 32];
-        const int tl = tbase + lane;                              // lane t: token tbase + t
-        mxl_n = lane < 16 * NSW && tl < M ? (mx ? (uint32_t)mx[(size_t)tl * G + g] : 1u) : 0u;
+        m_n = ms[tg * 64 + row];
+        mxl_n = lane < MT && lane < M ? (mx ? (uint32_t)mx[(size_t)lane * G + g] : 1u) : 0u;
     };
-    auto compute = [&](const int8_t* xd, const uint32_t* w, uint32_t mlo, uint32_t mhi, uint32_t mxl) {
+    v16i biasv;
+#pragma unroll
+    for (int r = 0; r < 16; r++) biasv[r] = (int)PF_BIAS;
+    auto compute = [&](const int8_t* xd, const uint32_t* w, uint32_t mr, uint32_t mxl, int slot) __attribute__((always_inline)) {
         uint32_t* mxw = mxs_s[wv];
-        if (lane < 16 * NSW) mxw[lane] = mxl;                   // read back below by this wave only (in order)
+        if (lane < MT) mxw[lane] = mxl;          // read back below by this wave only (LDS operations stay in order)
+        if (hf == 0 && lane < MT) {
+            xdig[(0 * MT + lane) * NS + slot] = (int8_t)(mxl & 127);
+            xdig[(1 * MT + lane) * NS + slot] = (int8_t)((mxl >> 7) & 127);
+            xdig[(2 * MT + lane) * NS + slot] = (int8_t)(mxl >> 14);
+        }
+        if (e == 0) {
+            wdig[(0 * 64 + row) * NS + slot] = (int8_t)(mr & 127);
+            wdig[(1 * 64 + row) * NS + slot] = (int8_t)((mr >> 7) & 127);
+            wdig[(2 * 64 + row) * NS + slot] = (int8_t)(mr >> 14);
+        }
 #pragma unroll
-        for (int t = 0; t < NSW; t++) {
-            const int R = 16 * t + max(aoff, 0);                  // this lane's A row (token) within the part
-            v16i d = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        for (int t = 0; t < TS; t++) {
+            const int R = 32 * t + l32;          // this lane's A row (token)
+            v16i d = biasv;
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const v4i z = {0, 0, 0, 0};
-                const v4i xa = aoff >= 0 ? *reinterpret_cast<const v4i*>(xd + R * 128 + ((c ^ ((R >> 1) & 7)) << 4)) : z;
-                const v4i bw = {(int)w[4 * c], (int)w[4 * c + 1], (int)w[4 * c + 2], (int)w[4 * c + 3]};
+            for (int s = 0; s < 4; s++) {
+                const v4i xa = *reinterpret_cast<const v4i*>(xd + R * 128 + (((4 * e + s) ^ ((R >> 1) & 7)) << 4));
+                const v4i bw = {(int)w[4 * s], (int)w[4 * s + 1], (int)w[4 * s + 2], (int)w[4 * s + 3]};
                 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, bw, d, 0, 0, 0);
             }
-            // register r = 4 q + e: A row i = 8 q + e (low half of the wave) or 8 q + 4 + e (high half); i < 16 is token
-            // i of row lane % 32, i >= 16 token i - 16 of row lane % 32 + 32.  So the four registers of q take four
-            // consecutive tokens from (8 q + 4 (lane / 32)) % 16, and row multiplier mlo (q < 2) or mhi (q >= 2).
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
-                const uint4 mv = *reinterpret_cast<const uint4*>(mxw + 16 * t + ((8 * qq + 4 * (lane >> 5)) & 15));
+                const uint4 mv = *reinterpret_cast<const uint4*>(mxw + 32 * t + 8 * qq + 4 * e);
                 const uint32_t mxv[4] = {mv.x, mv.y, mv.z, mv.w};
-                const uint32_t mrow = qq >= 2 ? mhi : mlo;
 #pragma unroll
-                for (int e = 0; e < 4; e++) mac_s32_u32(acc[t][4 * qq + e], d[4 * qq + e], mrow * mxv[e]);
+                for (int j = 0; j < 4; j++)
+                    U[t][4 * qq + j] += (unsigned long long)(uint32_t)d[4 * qq + j] * mul_u24(mr, mxv[j]);
             }
         }
     };
 
-    int g = g0 + slot;
-    if (g < g1) fetch(g, xa0);
-    for (int par = 0; g < g1; g += S, par ^= 1) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // group g's copies and loads have landed
-        uint32_t w[32];
+    int g = g0 + pr;
+    DMS_TR(62, 0);
+    if (g < g1) fetch(g, area(0));
+    for (int it = 0; it < rounds; it++, g += P) {
+        DMS_TR(it, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // this wave's copies and loads for round it have landed
+        DMS_TR(it, 1);
+        __syncthreads();                                      // ... and the other waves' copies
+        DMS_TR(it, 2);
+        uint32_t w[16];
 #pragma unroll
-        for (int b = 0; b < 4; b++) block_signed<BITS>(q + b * NC, w + 8 * b);
-        const uint32_t mlo = mlo_n, mhi = mhi_n, mxl = mxl_n;
-        const int8_t* xd = par ? xa1 : xa0;
-        if (g + S < g1) fetch(g + S, par ? xa0 : xa1);        // the next group's loads run under this compute
-        compute(xd, w, mlo, mhi, mxl);
+        for (int b = 0; b < 2; b++) block_signed<BITS>(q + b * NC, w + 8 * b);
+        const uint32_t mr = m_n, mxl = mxl_n;
+        if (g + P < g1) fetch(g + P, area((it + 1) & 1));   // the next round's loads run under this compute
+        DMS_TR(it, 3);
+        if (g < g1) compute(area(it & 1), w, mr, mxl, g - g0);
+        DMS_TR(it, 4);
     }
+    if (wv == 0 && lane < MT) sxs_s[lane] = sxl;
+    __syncthreads();                                          // digits staged, activation areas free
+    DMS_TR(63, 0);
+    // U -= B * S for block (row half hf, token set t) where t % P == pr:
+    // S = sum_{i,j} 2^(7 (i + j)) D_ij, D_ij = sum over slots of digit i of mx times digit j of m
 #pragma unroll
-    for (int t = 0; t < NSW; t++)
+    for (int t = 0; t < TS; t++) {
+        if (t % P != pr) continue;               // compile-time t: U is indexed by constants only
+        for (int k0 = 0; k0 < NS; k0 += 32) {
+            v4i A[3], Bd[3];
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-            if (g0 + slot < g1)
-                __hip_atomic_fetch_add(tot_s + ((tp * NSW + t) * 16 + r) * 64 + lane, acc[t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    __syncthreads();
-    // thread (wave w, lane) finishes registers R = w, w + W, ... of the sums
-    const size_t npad = (size_t)(gridDim.x / KS) * TILE_N;
-    if (KS > 1) {
-        for (int R = wv; R < MP; R += W) {
-            const int t = 16 * (R >> 4) + dec_tok<16>(R & 15, lane), n = tile * TILE_N + dec_row<16>(R & 15, lane);
-            if (t < M) __hip_atomic_fetch_add(part + (size_t)t * npad + n, tot_s[R * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < 3; i++) {
+                const int4 av = *reinterpret_cast<const int4*>(xdig + (i * MT + 32 * t + l32) * NS + k0 + 16 * e);
+                const int4 bv = *reinterpret_cast<const int4*>(wdig + (i * 64 + row) * NS + k0 + 16 * e);
+                const int s0 = k0 + 16 * e;
+                A[i][0] = mask_slots(av.x, s0, ng); A[i][1] = mask_slots(av.y, s0 + 4, ng);
+                A[i][2] = mask_slots(av.z, s0 + 8, ng); A[i][3] = mask_slots(av.w, s0 + 12, ng);
+                Bd[i][0] = mask_slots(bv.x, s0, ng); Bd[i][1] = mask_slots(bv.y, s0 + 4, ng);
+                Bd[i][2] = mask_slots(bv.z, s0 + 8, ng); Bd[i][3] = mask_slots(bv.w, s0 + 12, ng);
+            }
+            const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+            const v16i d4 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[2], z, 0, 0, 0);
+            v16i d3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[1], z, 0, 0, 0);
+            d3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[2], d3, 0, 0, 0);
+            v16i d2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[0], z, 0, 0, 0);
+            d2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[1], d2, 0, 0, 0);
+            d2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[2], d2, 0, 0, 0);
+            v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[0], z, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[1], d1, 0, 0, 0);
+            const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[0], z, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                // d4 < 2^13, d3 < 2^19, d2, d1 < 2^20, d0 < 2^19: the top part fits int32, the rest int64
+                const int hi = (d4[r] << 7) + d3[r];                                     // < 2^21
+                long long S = ((long long)hi << 7) + d2[r];
+                S = (S << 7) + d1[r];
+                S = (S << 7) + d0[r];
+                U[t][r] -= (unsigned long long)S << 21;
+            }
         }
-        __builtin_amdgcn_s_waitcnt(0);             // this wave's adds have been performed
+    }
+    DMS_TR(63, 1);
+    // sums of the workgroup: tot[t][row], pair 0 writes, the others add
+    long long* tot = reinterpret_cast<long long*>(xs_dyn);
+    if (pr == 0) {
+#pragma unroll
+        for (int t = 0; t < TS; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                tot[(32 * t + 8 * (r >> 2) + 4 * e + (r & 3)) * 64 + row] = (long long)U[t][r];
+    }
+    __syncthreads();
+    if (pr > 0) {
+#pragma unroll
+        for (int t = 0; t < TS; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                __hip_atomic_fetch_add(tot + (32 * t + 8 * (r >> 2) + 4 * e + (r & 3)) * 64 + row, (long long)U[t][r],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();
+    DMS_TR(63, 2);
+    // thread (wave w, lane) finishes tokens w + W i of row n (W = 2 or 4: at most MT / 2 of them), every load
+    // before the first conversion, every conversion before the first store
+    constexpr int EI = MT / 2;
+    const int mt = min(M, MT);
+    long long v[EI];
+#pragma unroll
+    for (int i = 0; i < EI; i++) {
+        const int t = wv + W * i;
+        v[i] = t < mt ? tot[t * 64 + lane] : 0;
+    }
+    if (KS > 1) {
+        const size_t npad = (size_t)(gridDim.x / KS) * TILE_N;
+        long long* mine = part + (size_t)ks * MT * npad;
+#pragma unroll
+        for (int i = 0; i < EI; i++) {
+            const int t = wv + W * i;
+            if (t < mt) __hip_atomic_store(mine + (size_t)t * npad + n, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);             // this wave's stores have been performed
         __syncthreads();
         if (threadIdx.x == 0)
             last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);
         __syncthreads();
         if (!last_s) return;
-        for (int R = wv; R < MP; R += W) {
-            const int t = 16 * (R >> 4) + dec_tok<16>(R & 15, lane), n = tile * TILE_N + dec_row<16>(R & 15, lane);
-            const long long v = t < M ? __hip_atomic_exchange(part + (size_t)t * npad + n, 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-            if (t < M && n < N) out.store(N, t, n, (i64_to_f(v) * cs[n]) * sx[t]);
+        for (int k = 0; k < KS; k++) {
+            if (k == ks) continue;
+            const long long* other = part + (size_t)k * MT * npad;
+            long long o[EI];
+#pragma unroll
+            for (int i = 0; i < EI; i++) {
+                const int t = wv + W * i;
+                o[i] = t < mt ? __hip_atomic_load(other + (size_t)t * npad + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+            }
+#pragma unroll
+            for (int i = 0; i < EI; i++) v[i] += o[i];
         }
         if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
     }
-    for (int R = wv; R < MP; R += W) {
-        const int t = 16 * (R >> 4) + dec_tok<16>(R & 15, lane), n = tile * TILE_N + dec_row<16>(R & 15, lane);
-        if (t < M && n < N) out.store(N, t, n, (i64_to_f(tot_s[R * 64 + lane]) * cs[n]) * sx[t]);
+    float f[EI];
+#pragma unroll
+    for (int i = 0; i < EI; i++) {
+        const int t = wv + W * i;
+        f[i] = (i64_to_f(v[i]) * cn) * sxs_s[t < MT ? t : 0];
     }
-}
-
-// ------------------------------------------------------------------ MFMA GEMM (16 < M <= 64)
-constexpr int MF_BN = 128;          // output rows n per workgroup (two 64-row tiles)
-constexpr int MF_STR = 144;         // LDS row stride in bytes (128 codes + 16 pad)
-
-template <int BITS, int BM>
-__global__ void __launch_bounds__(256) k_mfma(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
-                                               const uint16_t* __restrict__ ms, int N, int K,
-                                               const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                               const uint16_t* __restrict__ mx, int M, Out out) {
-    constexpr int NC = group_bytes(BITS) / 16;
-    constexpr int TM = BM / 64;                    // 32x32 tiles per wave along t
-    __shared__ __attribute__((aligned(16))) int8_t As[BM * MF_STR];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[MF_BN * MF_STR];
-    __shared__ uint32_t mxs[BM];
-
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv >> 1, wn = wv & 1;
-    const int n0 = blockIdx.x * MF_BN, t0 = blockIdx.y * BM;
-    const int G = K / GROUP;
-    const int tile0 = n0 / TILE_N;
-
-    long long acc[TM][2][16];
+    if (n >= N) return;
+    if (!out.acc && out.nparts <= 1) {
 #pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
-
-    for (int g = 0; g < G; g++) {
-        __syncthreads();
-        // activations: BM rows x 128 bytes
-#pragma unroll
-        for (int i = 0; i < BM / 32; i++) {
-            const int ch = tid + i * 256, tl = ch >> 3, kc = ch & 7;
-            const int t = t0 + tl;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (t < M) v = *reinterpret_cast<const uint4*>(xq + (size_t)t * K + (size_t)g * GROUP + kc * 16);
-            *reinterpret_cast<uint4*>(As + tl * MF_STR + kc * 16) = v;
+        for (int i = 0; i < EI; i++) {
+            const int t = wv + W * i;
+            if (t < mt) out.y[(size_t)t * N + n] = f[i];
         }
-        // weights: thread = (row r, half h) unpacks 64 codes
-        {
-            const int r = tid >> 1, h = tid & 1;
-            const int tile = tile0 + (r >> 6), rr = r & 63;
-            const uint4* src = reinterpret_cast<const uint4*>(wq + ((size_t)tile * G + g) * NC * 1024) + rr;
-            uint32_t q[NC * 2];
+    } else {
 #pragma unroll
-            for (int c = 0; c < NC / 2; c++) {
-                const uint4 v = src[(h * (NC / 2) + c) * 64];
-                q[4 * c] = v.x; q[4 * c + 1] = v.y; q[4 * c + 2] = v.z; q[4 * c + 3] = v.w;
-            }
-            uint32_t w[16];
-            block_signed<BITS>(q, w);
-            block_signed<BITS>(q + NC, w + 8);
-            uint4* dst = reinterpret_cast<uint4*>(Bs + r * MF_STR + h * 64);
-#pragma unroll
-            for (int c = 0; c < 4; c++) dst[c] = make_uint4(w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]);
-        }
-        if (tid < BM) {
-            const int t = t0 + tid;
-            mxs[tid] = (mx && t < M) ? (uint32_t)mx[(size_t)t * G + g] : 1u;
-        }
-        __syncthreads();
-
-        v16i c[TM][2];
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            v4i a[TM], b[2];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                a[i] = *reinterpret_cast<const v4i*>(As + (wm * (BM / 2) + i * 32 + (lane & 31)) * MF_STR + s * 32 + (lane >> 5) * 16);
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                b[j] = *reinterpret_cast<const v4i*>(Bs + (wn * 64 + j * 32 + (lane & 31)) * MF_STR + s * 32 + (lane >> 5) * 16);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                    c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], s == 0 ? z : c[i][j], 0, 0, 0);
-                }
-        }
-        // group scaling: element (row t, col n) of a 32x32 tile sits in lane (n % 32) + 32 * ((t / 4) % 2),
-        // register 4 * (t / 8) + t % 4
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int nl = wn * 64 + j * 32 + (lane & 31);
-            const uint32_t mm = ms[((size_t)(tile0 + (nl >> 6)) * G + g) * 64 + (nl & 63)];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int tl = wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    mac_s32_u32(acc[i][j][r], c[i][j][r], mm * mxs[tl]);
-                }
+        for (int i = 0; i < EI; i++) {
+            const int t = wv + W * i;
+            if (t < mt) out.store(N, t, n, f[i]);
         }
     }
-
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        if (n >= N) continue;
-        const float cn = cs[n];
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int t = t0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (t < M) out.store(N, t, n, (i64_to_f(acc[i][j][r]) * cn) * sx[t]);
-            }
-    }
+    DMS_TR(63, 3);
 }
 
 // ------------------------------------------------------------------ prefill MFMA GEMM (M > 64)
@@ -646,21 +684,13 @@ __global__ void __launch_bounds__(256) k_mfma(const uint8_t* __restrict__ wq, co
 //     S = 65536*D11 + 256*(D10 + D01) + D00 + 32896*(Ra[t] + Rb[n]) + G*32896^2,
 //     Dij = sum_g a_i[t,g] b_j[n,g],  Ra[t] = sum_g (mx - 32896),  Rb[n] = sum_g (m - 32896).
 constexpr int PF_BM = 128, PF_BN = 128;
-constexpr uint32_t PF_BIAS = 1u << 21;
-constexpr int DIG_C = 32896;
 
-__device__ __forceinline__ void digits16(uint32_t v, int& d1, int& d0) {
-    const int vp = (int)v - DIG_C;
-    d0 = ((vp + 128) & 255) - 128;
-    d1 = (vp - d0) >> 8;
-}
 // byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile
 // (chunk position c ^ ((r / 2) % 8): the 16 rows that one LDS cycle serves fall on 16 distinct 16-byte bank slots)
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
 
 #ifdef PF_TRACE
-__device__ unsigned long long g_trace[4 * 64 * 8];
 #define PF_TR(slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
     __builtin_amdgcn_sched_barrier(0); if (blockIdx.x < 4 && threadIdx.x == 0 && tr_hi < 64) g_trace[(blockIdx.x * 64 + tr_hi) * 8 + (slot)] = tr_; } while (0)
 #else
@@ -1177,34 +1207,44 @@ void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, cons
     DET_CHECK(hipGetLastError());
 }
 
-template <int BITS, int NSW, int TP>
+// K-slice partial sums of k_decode_ms: part[KS][MT][Npad] int64 (each slice stores its own plane, so no zeroing)
+long long* g_part_ms = nullptr;
+size_t g_part_ms_cap = 0;
+
+template <int BITS, int TS>
 void launch_decode_ms(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
+    constexpr int MT = 32 * TS;
     const int G = L.K / GROUP;
     const int T = (L.N + TILE_N - 1) / TILE_N;
     const int cus = g_decode_waves / 8;
-    int KS = 1;
-    if (2 * T < cus) KS = std::max(1, std::min((cus + T - 1) / T, (G + 3) / 4));
+    // K-slices until every CU has a workgroup (the second workgroup a CU holds overlaps the first's prologue and
+    // epilogue), each slice at most DMS_MAXSLOT groups
+    // K-slices until every CU has a workgroup, each slice keeping at least 16 groups (the slices' combine costs
+    // about as much as a few rounds) and at most DMS_MAXSLOT
+    int KS = T >= cus ? 1 : std::max(1, std::min((cus + T - 1) / T, G / 16));
+    KS = std::max(KS, (G + DMS_MAXSLOT - 1) / DMS_MAXSLOT);
     const int gs = (G + KS - 1) / KS;
-    // group slots per workgroup: enough waves for the device, each slot walking at least two groups so that the
-    // pipeline has something to overlap
-    int S = (g_decode_waves + T * KS * TP - 1) / (T * KS * TP);
-    S = std::max(1, std::min(S, std::min((gs + 1) / 2, 8 / TP)));
+    KS = (G + gs - 1) / gs;                      // no empty slices
+    // four pairs when every workgroup has a CU of its own, else two (two workgroups share a CU, one's prologue and
+    // epilogue overlapping the other's rounds)
+    const int P = std::min(T * KS <= cus ? DMS_MAXP : 2, gs);
     long long* part = nullptr;
     unsigned int* cnt = nullptr;
     if (KS > 1) {
-        decode_buffers((size_t)16 * NSW * TP * T * TILE_N, (size_t)T, st);
-        part = g_part;
+        const size_t need = (size_t)KS * MT * T * TILE_N;
+        if (need > g_part_ms_cap) {
+            DET_CHECK(hipStreamSynchronize(st));
+            if (g_part_ms) DET_CHECK(hipFree(g_part_ms));
+            g_part_ms_cap = std::max(need, (size_t)1 << 20);
+            DET_CHECK(hipMalloc(&g_part_ms, g_part_ms_cap * 8));
+        }
+        decode_buffers(0, (size_t)T, st);        // arrival counters (shared with k_decode: zero between calls)
+        part = g_part_ms;
         cnt = g_cnt;
     }
-    const size_t lds = (size_t)S * TP * 2 * 16 * NSW * 128;         // two activation areas per wave
-    k_decode_ms<BITS, NSW, TP><<<T * KS, 64 * S * TP, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
-    DET_CHECK(hipGetLastError());
-}
-
-template <int BITS, int BM>
-void launch_mfma(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
-    dim3 grid((L.N + MF_BN - 1) / MF_BN, (M + BM - 1) / BM);
-    k_mfma<BITS, BM><<<grid, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y);
+    const int NS = (gs + 31) & ~31;
+    const size_t lds = std::max((size_t)2 * P * MT * 128, (size_t)MT * TILE_N * 8) + (size_t)3 * (64 + MT) * NS;
+    k_decode_ms<BITS, TS><<<T * KS, 128 * P, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
     DET_CHECK(hipGetLastError());
 }
 
@@ -1216,8 +1256,8 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         else if (M <= 8) launch_decode<BITS, 8>(L, xq, sx, mx, M, y, st);
         else launch_decode<BITS, 16>(L, xq, sx, mx, M, y, st);
     } else if (M <= 64) {
-        if (M <= 32) launch_decode_ms<BITS, 2, 1>(L, xq, sx, mx, M, y, st);
-        else launch_decode_ms<BITS, 2, 2>(L, xq, sx, mx, M, y, st);
+        if (M <= 32) launch_decode_ms<BITS, 1>(L, xq, sx, mx, M, y, st);
+        else launch_decode_ms<BITS, 2>(L, xq, sx, mx, M, y, st);
     } else {
         const int nbn = (L.N + PF_BN - 1) / PF_BN, nbt = (M + PF_BM - 1) / PF_BM;
         k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
@@ -1256,7 +1296,7 @@ void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hi
     DET_CHECK(hipGetLastError());
 }
 
-#ifdef PF_TRACE
+#if defined(PF_TRACE) || defined(DMS_TRACE)
 void det_debug_trace(unsigned long long* host) {
     DET_CHECK(hipDeviceSynchronize());
     DET_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace)));

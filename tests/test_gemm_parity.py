@@ -213,3 +213,18 @@ def test_decode_every_m(bits):
                 xq, sx, mx = oracle.quant(x, group=group)
                 want = oracle.gemm(rows, n, k, bits, xq, sx, mx)
                 assert same_f32(want, run_gemm(lin, xq, sx, mx, m)) is None, f'n={n} m={m} group={group}'
+
+
+@pytest.mark.parametrize('bits', [6, 4])
+def test_decode_ms_long_k(bits):
+    """Token-set decode (16 < M <= 64) with more groups per wave than one 32-group digit step: n = 9000 rows fill the
+    device without a K-split, k = 17920 (140 groups) gives each wave 35 rounds, so the bias correction runs twice."""
+    rng = oracle.Rng(500 + bits)
+    n, k = 9000, 17920
+    rows = rng.fake_rows(bits, n, k)
+    lin = ffi.Linear(rows, k, bits)
+    for m in (20, 50):
+        print(f'decode_ms W{bits} n={n} k={k} m={m}', flush=True)
+        xq, sx, mx = oracle.quant(rng.acts_x(m, k))
+        want = oracle.gemm(rows, n, k, bits, xq, sx, mx)
+        assert same_f32(want, run_gemm(lin, xq, sx, mx, m)) is None, f'm={m}'
