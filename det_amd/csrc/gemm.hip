@@ -370,14 +370,14 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
     }
 }
 
-// balanced digits of a 16-bit multiplier: v = 256 d1 + d0 + 32896 with d1, d0 in [-128, 127]
+// start value of every MFMA chain in the biased scaling: |p| <= 128 * 127 * 128 < 2^21, so p + B >= 0
 constexpr uint32_t PF_BIAS = 1u << 21;
-constexpr int DIG_C = 32896;
-
-__device__ __forceinline__ void digits16(uint32_t v, int& d1, int& d0) {
-    const int vp = (int)v - DIG_C;
-    d0 = ((vp + 128) & 255) - 128;
-    d1 = (vp - d0) >> 8;
+// a * b for a, b < 2^16 (m and mx).  Inline asm: the compiler turns __umul24 of operands it cannot bound into an
+// AND and the quarter-rate v_mul_lo_u32.
+__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
 // ------------------------------------------------------------------ decode, many tokens (16 < M <= 64)
 // A workgroup of P (<= 4) wave pairs walks the groups g0 .. g1-1 of one tile's K-slice, pair p taking groups
@@ -408,11 +408,6 @@ __device__ unsigned long long g_trace[4 * 64 * 8];
 #else
 #define DMS_TR(h, slot) do {} while (0)
 #endif
-__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {   // exact for a, b < 2^24 with a * b < 2^32
-    uint32_t r;
-    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
 // bytes of v (slots s0 .. s0 + 3) at or past slot n set to zero
 __device__ __forceinline__ int mask_slots(int v, int s0, int n) {
     const int k = n - s0;
@@ -680,9 +675,8 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
 // accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
 //     U += (p + B) * (m * mx)            (v_mul_u32_u24, v_mad_u64_u32; exact, U < 2^62)
 // The bias is removed once per output: acc = U - B * S with S = sum_g m[n,g] * mx[t,g], computed exactly on the
-// MFMA from balanced int8 digits v = 256*v1 + v0 + 32896 (v1, v0 in [-128, 127]) of m and mx:
-//     S = 65536*D11 + 256*(D10 + D01) + D00 + 32896*(Ra[t] + Rb[n]) + G*32896^2,
-//     Dij = sum_g a_i[t,g] b_j[n,g],  Ra[t] = sum_g (mx - 32896),  Rb[n] = sum_g (m - 32896).
+// MFMA from unsigned 7-bit digits v = d0 + 128 d1 + 16384 d2 of m and mx, staged in LDS once per value:
+//     S = sum_{i,j} 2^(7 (i + j)) D_ij,   D_ij = sum_g dx_i[t,g] dw_j[n,g]   (every D_ij >= 0, no offset terms).
 constexpr int PF_BM = 128, PF_BN = 128;
 
 // byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile
@@ -751,7 +745,6 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                              : (uint32_t)((tile0 + ((tid - PF_BM) >> 6)) * G * 64 + ((tid - PF_BM) & 63)) * 2;
     const int s_step = xw ? 2 : 128;
     const bool x_one = xw && !(mx && t0 + tid < M);
-    int rsum = 0;          // Ra (tid < 128) or Rb (tid >= 128): sum over groups of (multiplier - 32896)
 
     // Global -> LDS copies by the buffer unit, in runs that share one M0 value.  Activations: one resource over xq,
     // copy i of wave wv takes rows t0 + 32 wv + 8 i + lane / 8 into As + 4096 wv + 1024 i (row r's chunk positions
@@ -799,9 +792,8 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         __builtin_amdgcn_sched_barrier(0);       // keep the wait after the scaling arithmetic of compute()
         asm volatile("s_waitcnt vmcnt(0)" : "+v"(sreg) :: "memory");
         PF_TR(3);
-        const uint32_t v = x_one ? 1u : sreg;
-        sdst[tid] = v;
-        rsum += real ? (int)v - DIG_C : 0;
+        sdst[tid] = x_one ? 1u : sreg;
+        (void)real;
         if (BITS != 8) {
             const int r = (wv >> 1) * 64 + lane, h = wv & 1;
             const uint8_t* pl = Bp + ((wv >> 1) * NC + h * (NC / 2)) * 1024 + lane * 16;
@@ -857,8 +849,7 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                 for (int e = 0; e < 4; e++)
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
-                        const uint32_t sc = __umul24(mcur[j], mxv[e]);
-                        U[i][j][4 * q4 + e] += (unsigned long long)(uint32_t)d[j][4 * q4 + e] * sc;
+                        U[i][j][4 * q4 + e] += (unsigned long long)(uint32_t)d[j][4 * q4 + e] * mul_u24(mcur[j], mxv[e]);
                     }
             }
             if (i == 0) mid();
@@ -898,87 +889,87 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         PF_TR(5);
     }
 
-    // ---- bias correction and epilogue.  S = sum_g m * mx comes from balanced digits on the MFMA, 32 groups at a
-    // time: the multipliers of those groups are staged in the (now idle) LDS buffers, xs[t][32] = mx and
-    // ws[n][32] = m (uint16), and U -= B * (65536 D11 + 256 (D10 + D01) + D00) is applied per step (it is linear).
+    // ---- bias correction and epilogue.  S = sum_g m * mx from 7-bit digits on the MFMA, 32 groups at a time: the
+    // digits of those groups' multipliers are staged in the (now idle) LDS buffers, xd[i][t][32] of mx and
+    // wd[i][n][32] of m, and U -= B * S is applied per step (it is linear).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     tr_hi = 63;
     PF_TR(0);
-    uint16_t* xs = reinterpret_cast<uint16_t*>(As0);            // PF_BM * 32 * 2 = 8 KB
-    uint16_t* ws = reinterpret_cast<uint16_t*>(Bs0);            // PF_BN * 32 * 2 = 8 KB
-    int* Ra = reinterpret_cast<int*>(As1);                      // sums of (mx - 32896) per token
-    int* Rb = Ra + PF_BM;                                       // sums of (m - 32896) per row
-    float* sxs = reinterpret_cast<float*>(Rb + PF_BN);          // sx of the tile's tokens
-    if (tid < PF_BM) {
-        Ra[tid] = rsum;
-        sxs[tid] = sx[min(t0 + tid, M - 1)];
-    } else {
-        Rb[tid - PF_BM] = rsum;
-    }
+    int8_t* xd = As0;                                           // [3][PF_BM][32] = 12 KB
+    int8_t* wd = Bs0;                                           // [3][PF_BN][32] = 12 KB
+    float* sxs = reinterpret_cast<float*>(As1);                 // sx of the tile's tokens
+    if (tid < PF_BM) sxs[tid] = sx[min(t0 + tid, M - 1)];
     // staging of 32 groups: thread tid loads 16 of them for token tid / 2 and for row tid / 2 (half tid % 2), all
-    // loads first, then the LDS writes (packed in pairs)
+    // loads first, then the digits, four values to a word (groups past G stage zero digits)
     const int sl = tid >> 1, sh = (tid & 1) * 16;
     const bool tok_ok = mx && t0 + sl < M;
     const uint16_t* mrow = mx + (size_t)(t0 + sl) * G;
     const uint16_t* wrow = ms + (size_t)(tile0 + (sl >> 6)) * G * 64 + (sl & 63);
+    // digits of four values < 2^16 as the bytes of three words (two values per word while extracting)
+    auto digits4 = [](const uint32_t* v, uint32_t& w0, uint32_t& w1, uint32_t& w2) __attribute__((always_inline)) {
+        const uint32_t p01 = v[0] | (v[1] << 16), p23 = v[2] | (v[3] << 16);
+        w0 = __builtin_amdgcn_perm(p23 & 0x007f007fu, p01 & 0x007f007fu, 0x06040200u);
+        w1 = __builtin_amdgcn_perm((p23 >> 7) & 0x007f007fu, (p01 >> 7) & 0x007f007fu, 0x06040200u);
+        w2 = __builtin_amdgcn_perm((p23 >> 14) & 0x00030003u, (p01 >> 14) & 0x00030003u, 0x06040200u);
+    };
     for (int k0 = 0; k0 < G; k0 += 32) {
         uint32_t xv[16], wv_[16];
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int g = k0 + sh + e;
-            // a multiplier of 32896 has zero digits: groups past G add nothing
-            xv[e] = g < G ? (tok_ok ? (uint32_t)mrow[g] : 1u) : (uint32_t)DIG_C;
-            wv_[e] = g < G ? (uint32_t)wrow[(size_t)g * 64] : (uint32_t)DIG_C;
+            xv[e] = g < G ? (tok_ok ? (uint32_t)mrow[g] : 1u) : 0u;
+            wv_[e] = g < G ? (uint32_t)wrow[(size_t)g * 64] : 0u;
+        }
+        uint32_t xw[3][4], ww[3][4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            digits4(xv + 4 * q, xw[0][q], xw[1][q], xw[2][q]);
+            digits4(wv_ + 4 * q, ww[0][q], ww[1][q], ww[2][q]);
         }
         PF_TR(6);
         __syncthreads();                     // the previous chunk's digit reads are done
 #pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-            *reinterpret_cast<uint32_t*>(xs + sl * 32 + sh + e) = xv[e] | (xv[e + 1] << 16);
-            *reinterpret_cast<uint32_t*>(ws + sl * 32 + sh + e) = wv_[e] | (wv_[e + 1] << 16);
+        for (int d = 0; d < 3; d++) {
+            *reinterpret_cast<uint4*>(xd + (d * PF_BM + sl) * 32 + sh) = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
+            *reinterpret_cast<uint4*>(wd + (d * PF_BN + sl) * 32 + sh) = make_uint4(ww[d][0], ww[d][1], ww[d][2], ww[d][3]);
         }
         __syncthreads();
-        v4i A1[2], A0[2], B1[2], B0[2];
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int ta = wm * 64 + i * 32 + l32;       // A-operand row (token) of this lane
-            const int nb = wn * 64 + i * 32 + l32;       // B-operand column (row n) for the j = i tile
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                uint32_t pa1 = 0, pa0 = 0, pb1 = 0, pb0 = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int gl = lh * 16 + 4 * w + e;
-                    int a1, a0, b1, b0;
-                    digits16(xs[ta * 32 + gl], a1, a0);
-                    digits16(ws[nb * 32 + gl], b1, b0);
-                    pa1 |= (uint32_t)(a1 & 255) << (8 * e);
-                    pa0 |= (uint32_t)(a0 & 255) << (8 * e);
-                    pb1 |= (uint32_t)(b1 & 255) << (8 * e);
-                    pb0 |= (uint32_t)(b0 & 255) << (8 * e);
-                }
-                A1[i][w] = (int)pa1; A0[i][w] = (int)pa0; B1[i][w] = (int)pb1; B0[i][w] = (int)pb0;
-            }
-        }
+        // one 32 x 32 block at a time, one digit weight at a time folded into t (few live registers next to U)
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++) {
+                v4i A[3], Bd[3];
+#pragma unroll
+                for (int d = 0; d < 3; d++) {
+                    A[d] = *reinterpret_cast<const v4i*>(xd + (d * PF_BM + wm * 64 + i * 32 + l32) * 32 + 16 * lh);
+                    Bd[d] = *reinterpret_cast<const v4i*>(wd + (d * PF_BN + wn * 64 + j * 32 + l32) * 32 + 16 * lh);
+                }
                 const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                const v16i d11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1[i], B1[j], z, 0, 0, 0);
-                v16i d1x = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1[i], B0[j], z, 0, 0, 0);
-                d1x = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0[i], B1[j], d1x, 0, 0, 0);
-                const v16i d00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0[i], B0[j], z, 0, 0, 0);
+                // digit weights 2^28 (sum < 2^9), 2^21 (< 2^15), 2^14 (< 2^21), 2^7 (< 2^20): t stays below 2^32
+                v16i t = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[2], z, 0, 0, 0);
+                v16i e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[1], z, 0, 0, 0);
+                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[2], e, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
+                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[0], z, 0, 0, 0);
+                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[1], e, 0, 0, 0);
+                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[2], e, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
+                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[0], z, 0, 0, 0);
+                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[1], e, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
+                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[0], z, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int t1 = (d11[r] << 8) + d1x[r];            // |t1| < 2^30
-                    const long long S = ((long long)t1 << 8) + d00[r];
-                    U[i][j][r] -= (unsigned long long)S << 21;
+                    const unsigned long long S = ((unsigned long long)(uint32_t)t[r] << 7) + (uint32_t)e[r];
+                    U[i][j][r] -= S << 21;
                 }
             }
     }
     PF_TR(1);
-    const long long GC2 = (long long)G * DIG_C * DIG_C;
     // epilogue, 16 outputs at a time.  A whole tile routed to one plain output needs no per-element checks;
     // Accumulate loads all 16 old values before the first store, so no store waits on a load.
     const bool full = t0 + PF_BM <= M && n0 + PF_BN <= N && out.nparts <= 1;
@@ -987,23 +978,17 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         const int nb = wn * 64 + j * 32 + l32;
         const int n = n0 + nb;
         const float cn = n < N ? cs[n] : 0.0f;
-        const int rb = Rb[nb];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             float v[16];
 #pragma unroll
             for (int q4 = 0; q4 < 4; q4++) {
                 const int trb = wm * 64 + i * 32 + 8 * q4 + 4 * lh;
-                const int4 ra = *reinterpret_cast<const int4*>(Ra + trb);
                 const float4 sv = *reinterpret_cast<const float4*>(sxs + trb);
-                const int rav[4] = {ra.x, ra.y, ra.z, ra.w};
                 const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const long long rest = (long long)DIG_C * (rav[e] + rb) + GC2;
-                    const long long acc = (long long)(U[i][j][4 * q4 + e] - ((unsigned long long)rest << 21));
-                    v[4 * q4 + e] = ((float)acc * cn) * svv[e];   // int64 -> fp32 rounds to nearest even
-                }
+                for (int e = 0; e < 4; e++)
+                    v[4 * q4 + e] = (i64_to_f((long long)U[i][j][4 * q4 + e]) * cn) * svv[e];
             }
             if (full) {
                 float* yb = out.y + (size_t)(t0 + wm * 64 + i * 32 + 4 * lh) * N + n;
