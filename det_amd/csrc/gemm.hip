@@ -678,6 +678,7 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
 // MFMA from unsigned 7-bit digits v = d0 + 128 d1 + 16384 d2 of m and mx, staged in LDS once per value:
 //     S = sum_{i,j} 2^(7 (i + j)) D_ij,   D_ij = sum_g dx_i[t,g] dw_j[n,g]   (every D_ij >= 0, no offset terms).
 constexpr int PF_BM = 128, PF_BN = 128;
+constexpr int P2_BM = 128;        // tokens per workgroup of k_prefill2
 
 // byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile
 // (chunk position c ^ ((r / 2) % 8): the 16 rows that one LDS cycle serves fall on 16 distinct 16-byte bank slots)
@@ -1023,6 +1024,291 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
     PF_TR(2);
 }
 
+// int64 -> fp32 (round to nearest even) for the epilogues: |v| < 2^52 is exact as a double (high word times 2^32
+// plus the low word, one fma), and the double -> float conversion then rounds once; larger magnitudes take
+// i64_to_f.
+__device__ __forceinline__ float i64_to_f_fast(long long v) {
+    const int hi = (int)(v >> 32);
+    if ((uint32_t)(hi + (1 << 20)) < (1u << 21)) {       // -2^52 <= v < 2^52
+        const double d = __builtin_fma((double)hi, 4294967296.0, (double)(uint32_t)v);
+        return (float)d;
+    }
+    return i64_to_f(v);
+}
+#ifdef P2_TRACE
+__device__ unsigned long long g_trace2[4 * 4 * 64 * 8];
+#define P2_TR(it, slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
+    __builtin_amdgcn_sched_barrier(0); if (blockIdx.x < 4 && lane == 0 && (it) < 64) \
+    g_trace2[((blockIdx.x * 4 + wv) * 64 + (it)) * 8 + (slot)] = tr_; } while (0)
+#else
+#define P2_TR(it, slot) do {} while (0)
+#endif
+// ------------------------------------------------------------------ prefill, 128 x 64 tiles (M > 64)
+// Workgroup tile 128 tokens x 64 rows (one weight tile), 4 waves of 32 tokens x 64 rows; up to three workgroups per
+// CU (<= 168 VGPRs, <= 50 KB LDS), so a CU holds 12 waves whose MFMA chains, scaling and copy waits interleave.
+// Per 128-group g (one round):
+//   - every wave waits for its own copies of round g and stages its multiplier; barrier;
+//   - W4/W6: the packed codes (single staging buffer) are unpacked into the signed tile Bs, one 32-code block per
+//     lane (wave = block, lane = row); barrier.  W8: the MFMA reads its B operand straight from the staging buffer
+//     (tile layout: plane c holds bytes 16 c .. 16 c + 15 of the 64 rows), which is double buffered;
+//   - the copies of group g + 1 are issued by the buffer unit into LDS in two runs per wave, the activations right
+//     after the first barrier and the codes after the second (so each run's M0 change finds the previous run long
+//     issued), the multipliers into a register;
+//   - 8 v_mfma_i32_32x32x32_i8 (two chains from the bias B) and the scaling U += (p + B) * (m * mx).
+// The bias is removed at the end from 7-bit digits of m and mx on the MFMA, as in k_prefill.
+template <int BITS>
+__global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
+                                                      const uint16_t* __restrict__ ms, int N, int K,
+                                                      const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                      const uint16_t* __restrict__ mx, int M,
+                                                      Out out, int nbn, int nbt) {
+    constexpr int NC = group_bytes(BITS) / 16;                 // 1 KB planes per tile-group
+    constexpr int WB = NC * 1024;
+    constexpr int NSTAGE = BITS == 8 ? 2 : 1;                  // W8 computes from the staging buffer
+    __shared__ __attribute__((aligned(16))) int8_t As[2][P2_BM * 128];
+    __shared__ __attribute__((aligned(16))) int8_t Bp[NSTAGE][WB];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[BITS == 8 ? 16 : TILE_N * 128];
+    __shared__ __attribute__((aligned(16))) uint32_t mxs[2][P2_BM];   // mx of the tile's tokens, per buffer
+    __shared__ uint16_t mss[2][TILE_N];                                // m of the tile's rows, per buffer
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);
+    const int l32 = lane & 31, lh = lane >> 5;
+    // XCD-aware order: consecutive workgroup ids go to different XCDs; each XCD gets a contiguous run of tiles,
+    // token blocks innermost, so the token blocks that share a weight tile share an L2
+    int tile = blockIdx.x;
+    const int total = nbn * nbt;
+    if ((total & 7) == 0) tile = (tile & 7) * (total >> 3) + (tile >> 3);
+    const int nb = tile / nbt, t0 = (tile % nbt) * P2_BM, n0 = nb * TILE_N;
+    const int G = K / GROUP;
+
+    unsigned long long U[2][16];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) U[j][r] = 0;
+    v16i biasv;
+#pragma unroll
+    for (int r = 0; r < 16; r++) biasv[r] = (int)PF_BIAS;
+
+    // activations: copy i of wave wv takes rows t0 + 32 wv + 8 i + lane / 8 into As + 4096 wv + 1024 i, row R's chunk
+    // c at position c ^ ((R / 2) % 8); copy i reads through its own resource (based 8 i rows on, minus the 1 KB
+    // instruction offset) whose range ends at row M, so rows past M read as zero
+    __amdgpu_buffer_rsrc_t xr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        xr[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(xq + (size_t)i * 8 * K - 1024 * i), (short)0,
+                                                  M > 8 * i ? (M - 8 * i) * K + 1024 * i : 0, 0x00020000);
+    const uint32_t a_vo = (uint32_t)(t0 + wv * 32 + (lane >> 3)) * (uint32_t)K + (uint32_t)(((lane & 7) ^ (lane >> 4)) * 16);
+    const uint32_t a_vo1 = a_vo ^ 64u;
+    // codes: the tile-group is WB contiguous bytes; wave w copies planes PW w .. PW w + PW - 1
+    constexpr int PW = BITS == 4 ? 1 : 2;
+    const bool w_copies = wvu * PW < NC;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)(wq + (size_t)nb * G * WB), (short)0, G * WB, 0x00020000);
+    const uint32_t w_vo[2] = {(uint32_t)lane * 16, (uint32_t)lane * 16};
+    // multipliers: thread tid < 128 loads mx of token t0 + tid, 128 <= tid < 192 m of row tid - 128
+    const bool xm = tid < P2_BM, wm_ = tid >= P2_BM && tid < P2_BM + TILE_N;
+    const __amdgpu_buffer_rsrc_t sr_x = __builtin_amdgcn_make_buffer_rsrc((void*)mx, (short)0, mx ? M * G * 2 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sr_w = __builtin_amdgcn_make_buffer_rsrc((void*)ms, (short)0, (nb + 1) * G * 128, 0x00020000);
+    const uint32_t s_vo = xm ? (uint32_t)(t0 + tid) * (uint32_t)G * 2 : (uint32_t)(nb * G * 64 + (tid - P2_BM)) * 2;
+    const bool x_one = xm && !(mx && t0 + tid < M);
+    uint32_t sreg = 1;
+
+    auto issue_a = [&](int g) __attribute__((always_inline)) {
+        dma16_run4x(xr, a_vo, a_vo1, g * GROUP, As[g & 1] + wvu * 4096);
+    };
+    auto issue_w = [&](int g) __attribute__((always_inline)) {
+        if (w_copies) dma16_run<PW>(wr, w_vo, g * WB + wvu * PW * 1024, Bp[NSTAGE == 2 ? (g & 1) : 0] + wvu * PW * 1024);
+        // uniform branches: one resource per wave
+        if (wvu < 2) sreg = __builtin_amdgcn_raw_buffer_load_b16(sr_x, s_vo, g * 2, 0);
+        else if (wvu == 2) sreg = __builtin_amdgcn_raw_buffer_load_b16(sr_w, s_vo, g * 128, 0);
+    };
+
+    P2_TR(63, 0);
+    issue_a(0);
+    issue_w(0);
+    for (int g = 0; g < G; g++) {
+        const int par = g & 1;
+        P2_TR(g, 0);
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(sreg) :: "memory");
+        P2_TR(g, 1);
+        if (xm) mxs[par][tid] = x_one ? 1u : sreg;
+        else if (wm_) mss[par][tid - P2_BM] = (uint16_t)sreg;
+        __syncthreads();                      // group g's copies have landed; group g - 1's compute is done
+        if (g + 1 < G) issue_a(g + 1);        // As[(g + 1) % 2] was last read by group g - 1's compute
+        P2_TR(g, 2);
+        if constexpr (BITS != 8) {
+            // unpack: wave = block b, lane = row; block b is bytes 8 NC/2... of the row's packed group
+            const int r = lane, b = wvu;
+            uint32_t q[6];
+            if constexpr (BITS == 6) {
+                const int8_t* p0 = Bp[0] + (3 * (b >> 1)) * 1024 + r * 16;
+                if ((b & 1) == 0) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(p0);
+                    const uint2 w = *reinterpret_cast<const uint2*>(p0 + 1024);
+                    q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w; q[4] = w.x; q[5] = w.y;
+                } else {
+                    const uint2 w = *reinterpret_cast<const uint2*>(p0 + 1024 + 8);
+                    const uint4 v = *reinterpret_cast<const uint4*>(p0 + 2048);
+                    q[0] = w.x; q[1] = w.y; q[2] = v.x; q[3] = v.y; q[4] = v.z; q[5] = v.w;
+                }
+            } else {
+                const uint4 v = *reinterpret_cast<const uint4*>(Bp[0] + b * 1024 + r * 16);
+                q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+            }
+            uint32_t o[8];
+            block_signed<BITS>(q, o);
+            *reinterpret_cast<uint4*>(Bs + swz(r, 2 * b)) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4*>(Bs + swz(r, 2 * b + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
+            __syncthreads();                  // Bs complete; the staging buffer is free again
+        }
+        P2_TR(g, 3);
+        if (g + 1 < G) issue_w(g + 1);        // W8: Bp[(g + 1) % 2] was last read by group g - 1's compute
+        P2_TR(g, 4);
+        // MFMA over group g and scaling into U
+        const int8_t* Ab = As[par];
+        v16i d[2];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const v4i a = *reinterpret_cast<const v4i*>(Ab + swz(wv * 32 + l32, 2 * s + lh));
+            v4i b0, b1;
+            if constexpr (BITS == 8) {
+                const int8_t* Bb = Bp[par] + (2 * s + lh) * 1024;
+                b0 = *reinterpret_cast<const v4i*>(Bb + l32 * 16);
+                b1 = *reinterpret_cast<const v4i*>(Bb + (32 + l32) * 16);
+            } else {
+                b0 = *reinterpret_cast<const v4i*>(Bs + swz(l32, 2 * s + lh));
+                b1 = *reinterpret_cast<const v4i*>(Bs + swz(32 + l32, 2 * s + lh));
+            }
+            d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, s == 0 ? biasv : d[0], 0, 0, 0);
+            d[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, s == 0 ? biasv : d[1], 0, 0, 0);
+        }
+        // element (t, n): lane n % 32 + 32 ((t / 4) % 2), register 4 (t / 8) + t % 4 of chain n / 32
+        const uint32_t m0 = mss[par][l32], m1 = mss[par][32 + l32];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const uint4 mv = *reinterpret_cast<const uint4*>(&mxs[par][wv * 32 + 8 * q4 + 4 * lh]);
+            const uint32_t mxv[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                U[0][4 * q4 + e] += (unsigned long long)(uint32_t)d[0][4 * q4 + e] * mul_u24(m0, mxv[e]);
+                U[1][4 * q4 + e] += (unsigned long long)(uint32_t)d[1][4 * q4 + e] * mul_u24(m1, mxv[e]);
+            }
+        }
+    }
+
+    P2_TR(63, 1);
+    // ---- bias correction: S = sum_g m * mx from 7-bit digits on the MFMA, 32 groups at a time, staged in As:
+    // xd[i][t][32] of mx (128 tokens), wd[i][n][32] of m (64 rows)
+    __syncthreads();                          // every wave is done with As
+    int8_t* xd = As[0];                       // [3][128][32] = 12 KB
+    int8_t* wd = As[1];                       // [3][64][32] = 6 KB
+    float* sxs = reinterpret_cast<float*>(As[1] + 8192);
+    if (tid < P2_BM) sxs[tid] = sx[min(t0 + tid, M - 1)];
+    // thread tid stages 16 groups of token tid / 2 (half tid % 2); threads < 128 also 16 groups of row tid / 2
+    const int sl = tid >> 1, sh = (tid & 1) * 16;
+    const bool tok_ok = mx && t0 + sl < M;
+    const uint16_t* mrow = mx + (size_t)(t0 + sl) * G;
+    const uint16_t* wrow = ms + (size_t)nb * G * 64 + (sl & 63);
+    auto digits4 = [](const uint32_t* v, uint32_t& w0, uint32_t& w1, uint32_t& w2) __attribute__((always_inline)) {
+        const uint32_t p01 = v[0] | (v[1] << 16), p23 = v[2] | (v[3] << 16);
+        w0 = __builtin_amdgcn_perm(p23 & 0x007f007fu, p01 & 0x007f007fu, 0x06040200u);
+        w1 = __builtin_amdgcn_perm((p23 >> 7) & 0x007f007fu, (p01 >> 7) & 0x007f007fu, 0x06040200u);
+        w2 = __builtin_amdgcn_perm((p23 >> 14) & 0x00030003u, (p01 >> 14) & 0x00030003u, 0x06040200u);
+    };
+    for (int k0 = 0; k0 < G; k0 += 32) {
+        uint32_t xv[16], wv_[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int g = k0 + sh + e;
+            xv[e] = g < G ? (tok_ok ? (uint32_t)mrow[g] : 1u) : 0u;
+            wv_[e] = g < G && tid < 2 * TILE_N ? (uint32_t)wrow[(size_t)g * 64] : 0u;
+        }
+        uint32_t xw[3][4], ww[3][4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            digits4(xv + 4 * q, xw[0][q], xw[1][q], xw[2][q]);
+            digits4(wv_ + 4 * q, ww[0][q], ww[1][q], ww[2][q]);
+        }
+        if (k0 > 0) __syncthreads();          // the previous chunk's digit reads are done
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+            *reinterpret_cast<uint4*>(xd + (d * P2_BM + sl) * 32 + sh) = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
+            if (tid < 2 * TILE_N)
+                *reinterpret_cast<uint4*>(wd + (d * TILE_N + sl) * 32 + sh) = make_uint4(ww[d][0], ww[d][1], ww[d][2], ww[d][3]);
+        }
+        __syncthreads();
+        v4i A[3];
+#pragma unroll
+        for (int d = 0; d < 3; d++) A[d] = *reinterpret_cast<const v4i*>(xd + (d * P2_BM + wv * 32 + l32) * 32 + 16 * lh);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            v4i Bd[3];
+#pragma unroll
+            for (int d = 0; d < 3; d++) Bd[d] = *reinterpret_cast<const v4i*>(wd + (d * TILE_N + j * 32 + l32) * 32 + 16 * lh);
+            const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+            // digit weights 2^28 (sum < 2^9), 2^21 (< 2^15), 2^14 (< 2^21), 2^7 (< 2^20): t stays below 2^32
+            v16i t = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[2], z, 0, 0, 0);
+            v16i e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[1], z, 0, 0, 0);
+            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[2], e, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
+            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[0], z, 0, 0, 0);
+            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[1], e, 0, 0, 0);
+            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[2], e, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
+            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[0], z, 0, 0, 0);
+            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[1], e, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
+            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[0], z, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const unsigned long long S = ((unsigned long long)(uint32_t)t[r] << 7) + (uint32_t)e[r];
+                U[j][r] -= S << 21;
+            }
+        }
+    }
+
+    P2_TR(63, 2);
+    // ---- epilogue: y = (f32(acc) * c[n]) * sx[t]; a tile routed whole to one plain output stores unchecked
+    const bool full = t0 + P2_BM <= M && n0 + TILE_N <= N && out.nparts <= 1;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int n = n0 + 32 * j + l32;
+        const float cn = n < N ? cs[n] : 0.0f;
+        float v[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const float4 sv = *reinterpret_cast<const float4*>(sxs + wv * 32 + 8 * q4 + 4 * lh);
+            const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[4 * q4 + e] = (i64_to_f_fast((long long)U[j][4 * q4 + e]) * cn) * svv[e];
+        }
+        const int tb = t0 + wv * 32 + 4 * lh;        // token of register 0; register r adds 8 (r / 4) + r % 4
+        if (full) {
+            float* yb = out.y + (size_t)tb * N + n;
+            if (out.acc) {
+                float old[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) old[r] = yb[(size_t)(8 * (r >> 2) + (r & 3)) * N];
+#pragma unroll
+                for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) yb[(size_t)(8 * (r >> 2) + (r & 3)) * N] = v[r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int t = tb + 8 * (r >> 2) + (r & 3);
+                if (t < M && n < N) out.store(N, t, n, v[r]);
+            }
+        }
+    }
+    P2_TR(63, 3);
+}
+
 // ------------------------------------------------------------------ load-time repack and quantizer
 __global__ void k_repack(const uint8_t* __restrict__ rows, int N, int K, int bits, uint8_t* __restrict__ wq,
                          float* __restrict__ cs, uint16_t* __restrict__ ms, size_t nchunks) {
@@ -1244,8 +1530,13 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         if (M <= 32) launch_decode_ms<BITS, 1>(L, xq, sx, mx, M, y, st);
         else launch_decode_ms<BITS, 2>(L, xq, sx, mx, M, y, st);
     } else {
+#ifdef PF_OLD
         const int nbn = (L.N + PF_BN - 1) / PF_BN, nbt = (M + PF_BM - 1) / PF_BM;
         k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
+#else
+        const int nbn = (L.N + TILE_N - 1) / TILE_N, nbt = (M + P2_BM - 1) / P2_BM;
+        k_prefill2<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
+#endif
         DET_CHECK(hipGetLastError());
     }
 }
@@ -1281,6 +1572,12 @@ void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hi
     DET_CHECK(hipGetLastError());
 }
 
+#if defined(P2_TRACE)
+void det_debug_trace2(unsigned long long* host) {
+    DET_CHECK(hipDeviceSynchronize());
+    DET_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace2), sizeof(g_trace2)));
+}
+#endif
 #if defined(PF_TRACE) || defined(DMS_TRACE)
 void det_debug_trace(unsigned long long* host) {
     DET_CHECK(hipDeviceSynchronize());
