@@ -18,7 +18,8 @@
 //       each lane half a row's packed group (no duplicate loads or unpacking); the activations come global -> LDS by
 //       the buffer unit; one v_mfma_i32_32x32x32_i8 per 32 codes and token set; group scaling with two VALU ops per
 //       output (biased partials, bias removed by digit-product MFMAs once per workgroup).
-//   k_prefill<BITS> (M > 64): 128 x 128 workgroup tiles, LDS double buffering, the same biased scaling.
+//   k_prefill2<BITS> (M > 64): 128-token x 64-row workgroup tiles, three workgroups per CU, activations copied
+//       global -> LDS by the buffer unit, the same biased scaling.
 #include <string.h>
 #include <algorithm>
 #include "common.h"
@@ -387,7 +388,7 @@ __device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
 // k-codes step s (0..3) the lane's B operand is its codes 64 e + 16 s .. + 15 and the A operand of lane l the same
 // codes of token l % 32 (+ 32 ts), so one v_mfma_i32_32x32x32_i8 per step and token set gives the 32 x 32 (token,
 // row) group partials in the standard layout: lane l keeps row 32 h + l % 32, register r token 8 (r / 4) + 4 e + r % 4.
-// Scaling as in k_prefill: each chain starts from B = 2^21 and U += (p + B) * (m * mx) (one v_mul_u32_u24, one
+// Scaling as in k_prefill2: each chain starts from B = 2^21 and U += (p + B) * (m * mx) (one v_mul_u32_u24, one
 // v_mad_u64_u32).  B * S, S = sum_g m * mx, is removed once per workgroup: every round stages the 7-bit digits of its
 // group's m (per row) and mx (per token) in LDS at the group's slot, and after the loop 9 digit-product MFMAs per 32
 // slots give S for each 32 x 32 block exactly.
@@ -399,7 +400,7 @@ __device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
 // `part`, counts itself in cnt[tile], and the last slice to arrive adds the other planes and writes the outputs.
 constexpr int DMS_MAXP = 4;          // wave pairs per workgroup
 constexpr int DMS_MAXSLOT = 96;      // groups per K-slice (digit slots in LDS)
-#if defined(PF_TRACE) || defined(DMS_TRACE)
+#if defined(DMS_TRACE)
 __device__ unsigned long long g_trace[4 * 64 * 8];
 #endif
 #ifdef DMS_TRACE
@@ -659,370 +660,12 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
     DMS_TR(63, 3);
 }
 
-// ------------------------------------------------------------------ prefill MFMA GEMM (M > 64)
-// Workgroup tile 128 tokens x 128 rows, 4 waves of 64 x 64 (2 x 2 v_mfma_i32_32x32x32_i8 tiles), two workgroups
-// per CU.  LDS holds two buffers of the activation tile and of the signed int8 weight tile, 128 rows of 128 bytes
-// each, with the 16-byte chunk c of row r stored at position c ^ ((r / 2) % 8), so that the 16 rows one LDS cycle
-// serves fall on distinct banks.  Per 128-group, while the MFMAs run on one buffer, the next group's activations
-// (and W8 codes) are copied global -> LDS by the buffer unit (buffer_load_dwordx4 ... lds, in runs of up to four
-// 1 KB copies under one M0 value) into the other buffer; W4/W6 codes land in a packed staging area that the same
-// wave unpacks into the other buffer (so one barrier per group suffices).  The activation run is issued before the
-// group's MFMAs, the weight run halfway through them.
-//
-// Build with -DPF_TRACE to record per-phase timestamps of four workgroups (det_debug_trace) for profiling.
-//
-// Group scaling with two VALU ops per (token, row, group): the first MFMA of a group starts from a constant
-// accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
-//     U += (p + B) * (m * mx)            (v_mul_u32_u24, v_mad_u64_u32; exact, U < 2^62)
-// The bias is removed once per output: acc = U - B * S with S = sum_g m[n,g] * mx[t,g], computed exactly on the
-// MFMA from unsigned 7-bit digits v = d0 + 128 d1 + 16384 d2 of m and mx, staged in LDS once per value:
-//     S = sum_{i,j} 2^(7 (i + j)) D_ij,   D_ij = sum_g dx_i[t,g] dw_j[n,g]   (every D_ij >= 0, no offset terms).
-constexpr int PF_BM = 128, PF_BN = 128;
+// ------------------------------------------------------------------ prefill (M > 64)
 constexpr int P2_BM = 128;        // tokens per workgroup of k_prefill2
 
 // byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile
 // (chunk position c ^ ((r / 2) % 8): the 16 rows that one LDS cycle serves fall on 16 distinct 16-byte bank slots)
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
-
-
-#ifdef PF_TRACE
-#define PF_TR(slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
-    __builtin_amdgcn_sched_barrier(0); if (blockIdx.x < 4 && threadIdx.x == 0 && tr_hi < 64) g_trace[(blockIdx.x * 64 + tr_hi) * 8 + (slot)] = tr_; } while (0)
-#else
-#define PF_TR(slot) do {} while (0)
-#endif
-template <int BITS>
-__global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
-                                                      const uint16_t* __restrict__ ms, int N, int K,
-                                                      const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                      const uint16_t* __restrict__ mx, int M,
-                                                      Out out, int nbn, int nbt) {
-    constexpr int NC = group_bytes(BITS) / 16;
-    constexpr int PK = BITS == 8 ? 16 : 2 * NC * 1024;         // packed staging bytes (W4/W6)
-    // Two buffers as distinct LDS objects, selected at compile time (the loop is unrolled by two), so that the
-    // compiler can see that reads of one buffer do not alias the global->LDS copies into the other and need not
-    // wait for them.
-    __shared__ __attribute__((aligned(16))) int8_t As0[PF_BM * 128], As1[PF_BM * 128];
-    __shared__ __attribute__((aligned(16))) int8_t Bs0[PF_BN * 128], Bs1[PF_BN * 128];
-    __shared__ __attribute__((aligned(16))) uint8_t Bp[PK];
-    // multipliers of the buffer's group: [0, 128) mx[t][g] of the tile's tokens, [128, 256) m[n][g] of its rows
-    __shared__ __attribute__((aligned(16))) uint32_t mul0[PF_BM + PF_BN], mul1[PF_BM + PF_BN];
-
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wvu = __builtin_amdgcn_readfirstlane(wv);        // the wave index as a scalar
-    const int wm = wv >> 1, wn = wv & 1;
-    // XCD-aware tile order: consecutive workgroup ids go to different XCDs; give each XCD a contiguous run of
-    // tiles (row-block major) so that the token blocks sharing one weight tile run on the same L2.
-    int tile = blockIdx.x;
-    const int total = nbn * nbt;
-    if ((total & 7) == 0) tile = (tile & 7) * (total >> 3) + (tile >> 3);
-    const int n0 = (tile / nbt) * PF_BN, t0 = (tile % nbt) * PF_BM;
-    const int G = K / GROUP;
-    const int tile0 = n0 / TILE_N;
-    const int l32 = lane & 31, lh = lane >> 5;
-
-    int tr_hi = 63;        // half-iteration index of the trace build (63: prologue and epilogue)
-    (void)tr_hi;
-    PF_TR(4);
-    unsigned long long U[2][2][16];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) U[i][j][r] = 0;
-
-    // weight copy: W8 straight into Bs (slot p = row r * 8 + position q takes chunk q ^ ((r / 2) % 8) of row r),
-    // W4/W6 into the Bp planes (wave wv: tile wv >> 1, chunk planes (wv & 1) * NC/2 .. +NC/2, which are exactly
-    // the half-groups this wave unpacks itself).  Per-lane addresses are 32-bit offsets from uniform bases.
-    const uint8_t* wbase = wq + (size_t)tile0 * G * NC * 1024;
-    // per-group multipliers: thread tid < 128 (waves 0, 1) stages mx of token t0 + tid, the others (waves 2, 3) m of
-    // row n0 + tid - 128, through buffer loads (the resource is uniform per wave); a missing mx (NULL) or a token
-    // past M reads as zero and stages 1.
-    const bool xw = wvu < 2;
-    const __amdgpu_buffer_rsrc_t sr = xw ? __builtin_amdgcn_make_buffer_rsrc((void*)mx, (short)0, mx ? M * G * 2 : 0, 0x00020000)
-                                         : __builtin_amdgcn_make_buffer_rsrc((void*)ms, (short)0, (tile0 + 2) * G * 128, 0x00020000);
-    const uint32_t s_vo = xw ? (uint32_t)(t0 + tid) * (uint32_t)G * 2
-                             : (uint32_t)((tile0 + ((tid - PF_BM) >> 6)) * G * 64 + ((tid - PF_BM) & 63)) * 2;
-    const int s_step = xw ? 2 : 128;
-    const bool x_one = xw && !(mx && t0 + tid < M);
-
-    // Global -> LDS copies by the buffer unit, in runs that share one M0 value.  Activations: one resource over xq,
-    // copy i of wave wv takes rows t0 + 32 wv + 8 i + lane / 8 into As + 4096 wv + 1024 i (row r's chunk positions
-    // swizzled by r % 8); the hardware range check returns zeros for rows past M.
-    // Copy i reads through its own resource, based 8 i rows further on minus the 1 KB instruction offset, so all four
-    // share one per-lane offset; its range ends at row M (rows past M read as zero).
-    __amdgpu_buffer_rsrc_t xr[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        xr[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(xq + (size_t)i * 8 * K - 1024 * i), (short)0,
-                                                  M > 8 * i ? (M - 8 * i) * K + 1024 * i : 0, 0x00020000);
-    // LDS row R = 32 wv + 8 i + lane / 8 keeps chunk (lane % 8) ^ ((R / 2) % 8) = (lane % 8) ^ (lane / 16) ^ 4 (i % 2)
-    const uint32_t a_vo = (uint32_t)(t0 + wv * 32 + (lane >> 3)) * (uint32_t)K + (uint32_t)(((lane & 7) ^ (lane >> 4)) * 16);
-    const uint32_t a_vo1 = a_vo ^ 64u;          // odd copies: chunk bit 2 flipped (a_vo's low 7 bits are the chunk)
-    // weights: W8 copy i of wave wv (tile wv / 2, rows 32 (wv % 2) + 8 i + lane / 8) into Bs + 4096 wv + 1024 i; the
-    // resource starts 4 KB before the tile pair so that the per-copy offsets stay non-negative.  W4/W6: the wave's
-    // NC/2 chunk planes of its tile, consecutive 1 KB in memory and in Bp.
-    const __amdgpu_buffer_rsrc_t wr = BITS == 8
-        ? __builtin_amdgcn_make_buffer_rsrc((void*)(wbase - 4096), (short)0, 2 * G * NC * 1024 + 4096, 0x00020000)
-        : __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, 2 * G * NC * 1024, 0x00020000);
-    uint32_t b_voff[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        b_voff[i] = BITS == 8 ? (uint32_t)(4096 + ((lane & 7) ^ (lane >> 4) ^ (4 * (i & 1))) * 1024 + (lane >> 3) * 16 + (wv & 1) * 512 + 128 * i - 1024 * i)
-                              : (uint32_t)lane * 16;
-    // registers filled by the copies of one group: the thread's multiplier and its token's first accumulator (W4/W6)
-    uint32_t sreg = 1;
-    // copies of group g, in two runs with their own M0 value: the activations (issued first), then the weight codes
-    // and the multiplier (issued halfway through the current group's MFMAs); nothing waits here
-    auto issue_a = [&](int g, int8_t* As) {
-        dma16_run4x(xr, a_vo, a_vo1, g * GROUP, As + wvu * 4096);
-    };
-    auto issue_w = [&](int g, int8_t* Bs) {
-        if (BITS == 8)
-            dma16_run<4>(wr, b_voff, ((wvu >> 1) * G + g) * NC * 1024, Bs + wvu * 4096);
-        else
-            dma16_run<NC / 2>(wr, b_voff, (((wvu >> 1) * G + g) * NC + (wvu & 1) * (NC / 2)) * 1024,
-                              Bp + ((wvu >> 1) * NC + (wvu & 1) * (NC / 2)) * 1024);
-        // a compiler-tracked load: an asm load's destination may be copied by the compiler before the data lands
-        sreg = __builtin_amdgcn_raw_buffer_load_b16(sr, s_vo, g * s_step, 0);
-    };
-    // wait for this wave's copies, stage the multiplier and unpack W4/W6 codes into the signed-int8 tile Bs (the
-    // wave reads only the staging planes its own copies wrote); the barrier follows
-    auto finish = [&](int8_t* Bs, uint32_t* sdst, bool real) {
-        __builtin_amdgcn_sched_barrier(0);       // keep the wait after the scaling arithmetic of compute()
-        asm volatile("s_waitcnt vmcnt(0)" : "+v"(sreg) :: "memory");
-        PF_TR(3);
-        sdst[tid] = x_one ? 1u : sreg;
-        (void)real;
-        if (BITS != 8) {
-            const int r = (wv >> 1) * 64 + lane, h = wv & 1;
-            const uint8_t* pl = Bp + ((wv >> 1) * NC + h * (NC / 2)) * 1024 + lane * 16;
-            uint32_t q[2 * NC];
-#pragma unroll
-            for (int c = 0; c < NC / 2; c++) {       // 16-byte chunk reads: a wave reads 1 KB contiguous
-                const uint4 v4 = *reinterpret_cast<const uint4*>(pl + c * 1024);
-                q[4 * c] = v4.x; q[4 * c + 1] = v4.y; q[4 * c + 2] = v4.z; q[4 * c + 3] = v4.w;
-            }
-#pragma unroll
-            for (int blk = 0; blk < 2; blk++) {
-                uint32_t o[8];
-                block_signed<BITS>(q + blk * NC, o);
-                *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2)) = make_uint4(o[0], o[1], o[2], o[3]);
-                *reinterpret_cast<uint4*>(Bs + swz(r, h * 4 + blk * 2 + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
-            }
-        }
-    };
-    // MFMA over one group from (As, Bs) and scaling into U
-    auto compute = [&](const int8_t* As, const int8_t* Bs, const uint32_t* mxs, const uint32_t* mss, auto&& mid) {
-        // every chain starts from the bias B (the tiles hold signed codes)
-        auto cinit_of = [&](int) {
-            v16i c;
-#pragma unroll
-            for (int r = 0; r < 16; r++) asm volatile("v_mov_b32 %0, %1" : "=v"(c[r]) : "i"(PF_BIAS));
-            return c;
-        };
-        // one token tile at a time: its two n-tiles' MFMA chains (32 accumulator registers), then their scaling
-        const uint32_t mcur[2] = {mss[wn * 64 + l32], mss[wn * 64 + 32 + l32]};
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            v16i d[2];
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                const v4i b0 = *reinterpret_cast<const v4i*>(Bs + swz(wn * 64 + l32, 2 * s + lh));
-                const v4i b1 = *reinterpret_cast<const v4i*>(Bs + swz(wn * 64 + 32 + l32, 2 * s + lh));
-                const v4i a = *reinterpret_cast<const v4i*>(As + swz(wm * 64 + i * 32 + l32, 2 * s + lh));
-                if (s == 0) {
-                    const v16i c = cinit_of(i);
-                    d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, c, 0, 0, 0);
-                    d[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, c, 0, 0, 0);
-                } else {
-                    d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, d[0], 0, 0, 0);
-                    d[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, d[1], 0, 0, 0);
-                }
-            }
-            // element (t, n) of a 32x32 tile: lane (n % 32) + 32 * ((t / 4) % 2), register 4 * (t / 8) + t % 4
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                const uint4 mv = *reinterpret_cast<const uint4*>(mxs + wm * 64 + i * 32 + 8 * q4 + 4 * lh);
-                const uint32_t mxv[4] = {mv.x, mv.y, mv.z, mv.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        U[i][j][4 * q4 + e] += (unsigned long long)(uint32_t)d[j][4 * q4 + e] * mul_u24(mcur[j], mxv[e]);
-                    }
-            }
-            if (i == 0) mid();
-        }
-    };
-
-    // The copy of the next group is issued unconditionally (past the last group it re-reads group G-1 into the
-    // idle buffer), so each half-iteration is one basic block and the scheduling barriers hold.
-    issue_a(0, As0);
-    issue_w(0, Bs0);
-    finish(Bs0, mul0, true);
-    __syncthreads();
-    PF_TR(5);
-    for (int g = 0; g < G; g += 2) {
-        tr_hi = g;
-        PF_TR(0);
-        const int g1 = g + 1;          // nothing to copy after the last group
-        if (g1 < G) issue_a(g1, As1);
-        PF_TR(1);
-        compute(As0, Bs0, mul0, mul0 + PF_BM, [&] { if (g1 < G) issue_w(g1, Bs1); });
-        PF_TR(2);
-        finish(Bs1, mul1, g1 < G);
-        PF_TR(4);
-        __syncthreads();
-        PF_TR(5);
-        if (g1 >= G) break;
-        tr_hi = g1;
-        PF_TR(0);
-        const int g2 = g + 2;
-        if (g2 < G) issue_a(g2, As0);
-        PF_TR(1);
-        compute(As1, Bs1, mul1, mul1 + PF_BM, [&] { if (g2 < G) issue_w(g2, Bs0); });
-        PF_TR(2);
-        finish(Bs0, mul0, g2 < G);
-        PF_TR(4);
-        __syncthreads();
-        PF_TR(5);
-    }
-
-    // ---- bias correction and epilogue.  S = sum_g m * mx from 7-bit digits on the MFMA, 32 groups at a time: the
-    // digits of those groups' multipliers are staged in the (now idle) LDS buffers, xd[i][t][32] of mx and
-    // wd[i][n][32] of m, and U -= B * S is applied per step (it is linear).
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    tr_hi = 63;
-    PF_TR(0);
-    int8_t* xd = As0;                                           // [3][PF_BM][32] = 12 KB
-    int8_t* wd = Bs0;                                           // [3][PF_BN][32] = 12 KB
-    float* sxs = reinterpret_cast<float*>(As1);                 // sx of the tile's tokens
-    if (tid < PF_BM) sxs[tid] = sx[min(t0 + tid, M - 1)];
-    // staging of 32 groups: thread tid loads 16 of them for token tid / 2 and for row tid / 2 (half tid % 2), all
-    // loads first, then the digits, four values to a word (groups past G stage zero digits)
-    const int sl = tid >> 1, sh = (tid & 1) * 16;
-    const bool tok_ok = mx && t0 + sl < M;
-    const uint16_t* mrow = mx + (size_t)(t0 + sl) * G;
-    const uint16_t* wrow = ms + (size_t)(tile0 + (sl >> 6)) * G * 64 + (sl & 63);
-    // digits of four values < 2^16 as the bytes of three words (two values per word while extracting)
-    auto digits4 = [](const uint32_t* v, uint32_t& w0, uint32_t& w1, uint32_t& w2) __attribute__((always_inline)) {
-        const uint32_t p01 = v[0] | (v[1] << 16), p23 = v[2] | (v[3] << 16);
-        w0 = __builtin_amdgcn_perm(p23 & 0x007f007fu, p01 & 0x007f007fu, 0x06040200u);
-        w1 = __builtin_amdgcn_perm((p23 >> 7) & 0x007f007fu, (p01 >> 7) & 0x007f007fu, 0x06040200u);
-        w2 = __builtin_amdgcn_perm((p23 >> 14) & 0x00030003u, (p01 >> 14) & 0x00030003u, 0x06040200u);
-    };
-    for (int k0 = 0; k0 < G; k0 += 32) {
-        uint32_t xv[16], wv_[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int g = k0 + sh + e;
-            xv[e] = g < G ? (tok_ok ? (uint32_t)mrow[g] : 1u) : 0u;
-            wv_[e] = g < G ? (uint32_t)wrow[(size_t)g * 64] : 0u;
-        }
-        uint32_t xw[3][4], ww[3][4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            digits4(xv + 4 * q, xw[0][q], xw[1][q], xw[2][q]);
-            digits4(wv_ + 4 * q, ww[0][q], ww[1][q], ww[2][q]);
-        }
-        PF_TR(6);
-        __syncthreads();                     // the previous chunk's digit reads are done
-#pragma unroll
-        for (int d = 0; d < 3; d++) {
-            *reinterpret_cast<uint4*>(xd + (d * PF_BM + sl) * 32 + sh) = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
-            *reinterpret_cast<uint4*>(wd + (d * PF_BN + sl) * 32 + sh) = make_uint4(ww[d][0], ww[d][1], ww[d][2], ww[d][3]);
-        }
-        __syncthreads();
-        // one 32 x 32 block at a time, one digit weight at a time folded into t (few live registers next to U)
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                v4i A[3], Bd[3];
-#pragma unroll
-                for (int d = 0; d < 3; d++) {
-                    A[d] = *reinterpret_cast<const v4i*>(xd + (d * PF_BM + wm * 64 + i * 32 + l32) * 32 + 16 * lh);
-                    Bd[d] = *reinterpret_cast<const v4i*>(wd + (d * PF_BN + wn * 64 + j * 32 + l32) * 32 + 16 * lh);
-                }
-                const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                // digit weights 2^28 (sum < 2^9), 2^21 (< 2^15), 2^14 (< 2^21), 2^7 (< 2^20): t stays below 2^32
-                v16i t = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[2], z, 0, 0, 0);
-                v16i e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[1], z, 0, 0, 0);
-                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[2], e, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
-                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[0], z, 0, 0, 0);
-                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[1], e, 0, 0, 0);
-                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[2], e, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
-                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[0], z, 0, 0, 0);
-                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[1], e, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
-                e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[0], z, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const unsigned long long S = ((unsigned long long)(uint32_t)t[r] << 7) + (uint32_t)e[r];
-                    U[i][j][r] -= S << 21;
-                }
-            }
-    }
-    PF_TR(1);
-    // epilogue, 16 outputs at a time.  A whole tile routed to one plain output needs no per-element checks;
-    // Accumulate loads all 16 old values before the first store, so no store waits on a load.
-    const bool full = t0 + PF_BM <= M && n0 + PF_BN <= N && out.nparts <= 1;
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int nb = wn * 64 + j * 32 + l32;
-        const int n = n0 + nb;
-        const float cn = n < N ? cs[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            float v[16];
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                const int trb = wm * 64 + i * 32 + 8 * q4 + 4 * lh;
-                const float4 sv = *reinterpret_cast<const float4*>(sxs + trb);
-                const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    v[4 * q4 + e] = (i64_to_f((long long)U[i][j][4 * q4 + e]) * cn) * svv[e];
-            }
-            if (full) {
-                float* yb = out.y + (size_t)(t0 + wm * 64 + i * 32 + 4 * lh) * N + n;
-                if (out.acc) {
-                    float old[16];
-#pragma unroll
-                    for (int r = 0; r < 16; r++) old[r] = yb[(size_t)(8 * (r >> 2) + (r & 3)) * N];
-#pragma unroll
-                    for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
-                }
-#pragma unroll
-                for (int r = 0; r < 16; r++) yb[(size_t)(8 * (r >> 2) + (r & 3)) * N] = v[r];
-            } else {
-                if (out.acc) {
-                    float old[16];
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                        old[r] = (t < M && n < N) ? *out.ptr(N, t, n) : 0.0f;
-                    }
-#pragma unroll
-                    for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
-                }
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int t = t0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (t < M && n < N) *out.ptr(N, t, n) = v[r];
-                }
-            }
-        }
-    }
-    PF_TR(2);
-}
 
 // int64 -> fp32 (round to nearest even) for the epilogues: |v| < 2^52 is exact as a double (high word times 2^32
 // plus the low word, one fma), and the double -> float conversion then rounds once; larger magnitudes take
@@ -1055,7 +698,12 @@ __device__ unsigned long long g_trace2[4 * 4 * 64 * 8];
 //     after the first barrier and the codes after the second (so each run's M0 change finds the previous run long
 //     issued), the multipliers into a register;
 //   - 8 v_mfma_i32_32x32x32_i8 (two chains from the bias B) and the scaling U += (p + B) * (m * mx).
-// The bias is removed at the end from 7-bit digits of m and mx on the MFMA, as in k_prefill.
+// Group scaling with two VALU ops per (token, row, group): each group's MFMA chain starts from a constant
+// accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
+//     U += (p + B) * (m * mx)            (v_mul_u32_u24, v_mad_u64_u32; exact, U < 2^62)
+// The bias is removed once per output, acc = U - B * S with S = sum_g m[n,g] * mx[t,g], computed exactly on the
+// MFMA from unsigned 7-bit digits v = d0 + 128 d1 + 16384 d2 of m and mx, staged in LDS once per value:
+//     S = sum_{i,j} 2^(7 (i + j)) D_ij,   D_ij = sum_g dx_i[t,g] dw_j[n,g]   (every D_ij >= 0, no offset terms).
 template <int BITS>
 __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                       const uint16_t* __restrict__ ms, int N, int K,
@@ -1530,13 +1178,8 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         if (M <= 32) launch_decode_ms<BITS, 1>(L, xq, sx, mx, M, y, st);
         else launch_decode_ms<BITS, 2>(L, xq, sx, mx, M, y, st);
     } else {
-#ifdef PF_OLD
-        const int nbn = (L.N + PF_BN - 1) / PF_BN, nbt = (M + PF_BM - 1) / PF_BM;
-        k_prefill<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
-#else
         const int nbn = (L.N + TILE_N - 1) / TILE_N, nbt = (M + P2_BM - 1) / P2_BM;
         k_prefill2<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
-#endif
         DET_CHECK(hipGetLastError());
     }
 }
@@ -1578,7 +1221,7 @@ void det_debug_trace2(unsigned long long* host) {
     DET_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace2), sizeof(g_trace2)));
 }
 #endif
-#if defined(PF_TRACE) || defined(DMS_TRACE)
+#if defined(DMS_TRACE)
 void det_debug_trace(unsigned long long* host) {
     DET_CHECK(hipDeviceSynchronize());
     DET_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace)));
