@@ -17,9 +17,21 @@ SRC = os.path.join(HERE, 'det_oracle.c')
 CFLAGS = ['-O2', '-fPIC', '-shared', '-ffp-contract=off', '-fno-fast-math', '-fopenmp', '-Wall']
 
 
+X86_SRC = os.path.join(HERE, 'x86_gemm.c')
+
+
 def build():
-    """Compile the C restatement (gcc, default MXCSR: no -ffast-math, no FMA contraction)."""
-    subprocess.check_call(['gcc'] + CFLAGS + ['-o', LIB_PATH, SRC, '-lm'])
+    """Compile the C restatement (gcc, default MXCSR: no -ffast-math, no FMA contraction) together with the
+    restatement of det's x86 GEMM (x86_gemm.c, built once for AVX2 and once for AVX2 + AVX-VNNI)."""
+    import tempfile
+    with tempfile.TemporaryDirectory() as tmp:
+        objs = []
+        for vnni, isa in ((0, ['-mavx2']), (1, ['-mavx2', '-mavxvnni'])):
+            o = os.path.join(tmp, f'x86_{vnni}.o')
+            subprocess.check_call(['gcc', '-O3', '-fPIC', '-fopenmp', '-Wall', '-c', f'-DXVNNI={vnni}'] + isa +
+                                  ['-o', o, X86_SRC])
+            objs.append(o)
+        subprocess.check_call(['gcc'] + CFLAGS + ['-o', LIB_PATH, SRC] + objs + ['-lm'])
 
 
 _lib = None
@@ -181,3 +193,38 @@ class Rng:
         out = np.zeros((m, k), np.float32)
         lib().ora_acts_x(self._sp(), m, k, _p(out))
         return out
+
+
+class X86Linear:
+    """det's x86 backend GEMM (crates/det/src/x86/gemm.rs) restated in C: the CPU baseline's timed path."""
+
+    def __init__(self, rows, N, K, bits):
+        L = lib()
+        L.ora_x86_repack.restype = ctypes.c_void_p
+        L.ora_x86_repack.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.ora_x86_gemm.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+        L.ora_x86_free.argtypes = [ctypes.c_void_p]
+        rows = np.ascontiguousarray(rows, dtype=np.uint8)
+        self.N, self.K, self.bits = N, K, bits
+        self.h = L.ora_x86_repack(_p(rows), N, K, bits)
+
+    def gemm(self, xq, sx, mx, vnni=None, threads=0):
+        if vnni is None:
+            vnni = has_vnni()
+        xq = np.ascontiguousarray(xq, dtype=np.int8)
+        sx = np.ascontiguousarray(sx, dtype=np.float32)
+        mx = None if mx is None else np.ascontiguousarray(mx, dtype=np.uint16)
+        M = xq.shape[0]
+        y = np.zeros((M, self.N), np.float32)
+        lib().ora_x86_gemm(self.h, _p(xq), _p(sx), _p(mx), M, _p(y), int(vnni), threads)
+        return y
+
+    def __del__(self):
+        if getattr(self, 'h', None):
+            lib().ora_x86_free(self.h)
+            self.h = None
+
+
+def has_vnni():
+    """AVX-VNNI (the VEX vpdpbusd det's x86 backend uses, x86/mod.rs:41-52) on this CPU."""
+    return bool(lib().ora_x86_has_vnni())
