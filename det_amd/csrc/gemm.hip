@@ -709,7 +709,8 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
                                                       const uint16_t* __restrict__ ms, int N, int K,
                                                       const int8_t* __restrict__ xq, const float* __restrict__ sx,
                                                       const uint16_t* __restrict__ mx, int M,
-                                                      Out out, int nbn, int nbt) {
+                                                      Out out, int nbn, int nbt, int KS,
+                                                      long long* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int NC = group_bytes(BITS) / 16;                 // 1 KB planes per tile-group
     constexpr int WB = NC * 1024;
     constexpr int NSTAGE = BITS == 8 ? 2 : 1;                  // W8 computes from the staging buffer
@@ -718,17 +719,21 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
     __shared__ __attribute__((aligned(16))) int8_t Bs[BITS == 8 ? 16 : TILE_N * 128];
     __shared__ __attribute__((aligned(16))) uint32_t mxs[2][P2_BM];   // mx of the tile's tokens, per buffer
     __shared__ uint16_t mss[2][TILE_N];                                // m of the tile's rows, per buffer
+    __shared__ unsigned int last_s;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wvu = __builtin_amdgcn_readfirstlane(wv);
     const int l32 = lane & 31, lh = lane >> 5;
     // XCD-aware order: consecutive workgroup ids go to different XCDs; each XCD gets a contiguous run of tiles,
-    // token blocks innermost, so the token blocks that share a weight tile share an L2
+    // token blocks innermost, so the token blocks that share a weight tile (and K-slice) share an L2
     int tile = blockIdx.x;
-    const int total = nbn * nbt;
+    const int total = nbn * nbt * KS;
     if ((total & 7) == 0) tile = (tile & 7) * (total >> 3) + (tile >> 3);
-    const int nb = tile / nbt, t0 = (tile % nbt) * P2_BM, n0 = nb * TILE_N;
+    const int nb = tile / (nbt * KS), rem = tile - nb * (nbt * KS), ks = rem / nbt, tb = rem - ks * nbt;
+    const int t0 = tb * P2_BM, n0 = nb * TILE_N;
     const int G = K / GROUP;
+    const int gs = (G + KS - 1) / KS;                          // groups of this workgroup's K-slice: [g0, g1)
+    const int g0 = ks * gs, g1 = min(G, g0 + gs);
 
     unsigned long long U[2][16];
 #pragma unroll
@@ -773,9 +778,9 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
     };
 
     P2_TR(63, 0);
-    issue_a(0);
-    issue_w(0);
-    for (int g = 0; g < G; g++) {
+    issue_a(g0);
+    issue_w(g0);
+    for (int g = g0; g < g1; g++) {
         const int par = g & 1;
         P2_TR(g, 0);
         asm volatile("s_waitcnt vmcnt(0)" : "+v"(sreg) :: "memory");
@@ -783,7 +788,7 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
         if (xm) mxs[par][tid] = x_one ? 1u : sreg;
         else if (wm_) mss[par][tid - P2_BM] = (uint16_t)sreg;
         __syncthreads();                      // group g's copies have landed; group g - 1's compute is done
-        if (g + 1 < G) issue_a(g + 1);        // As[(g + 1) % 2] was last read by group g - 1's compute
+        if (g + 1 < g1) issue_a(g + 1);       // As[(g + 1) % 2] was last read by group g - 1's compute
         P2_TR(g, 2);
         if constexpr (BITS != 8) {
             // unpack: wave = block b, lane = row; block b is bytes 8 NC/2... of the row's packed group
@@ -811,7 +816,7 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
             __syncthreads();                  // Bs complete; the staging buffer is free again
         }
         P2_TR(g, 3);
-        if (g + 1 < G) issue_w(g + 1);        // W8: Bp[(g + 1) % 2] was last read by group g - 1's compute
+        if (g + 1 < g1) issue_w(g + 1);       // W8: Bp[(g + 1) % 2] was last read by group g - 1's compute
         P2_TR(g, 4);
         // MFMA over group g and scaling into U
         const int8_t* Ab = As[par];
@@ -864,13 +869,13 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
         w1 = __builtin_amdgcn_perm((p23 >> 7) & 0x007f007fu, (p01 >> 7) & 0x007f007fu, 0x06040200u);
         w2 = __builtin_amdgcn_perm((p23 >> 14) & 0x00030003u, (p01 >> 14) & 0x00030003u, 0x06040200u);
     };
-    for (int k0 = 0; k0 < G; k0 += 32) {
+    for (int k0 = g0; k0 < g1; k0 += 32) {
         uint32_t xv[16], wv_[16];
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int g = k0 + sh + e;
-            xv[e] = g < G ? (tok_ok ? (uint32_t)mrow[g] : 1u) : 0u;
-            wv_[e] = g < G && tid < 2 * TILE_N ? (uint32_t)wrow[(size_t)g * 64] : 0u;
+            xv[e] = g < g1 ? (tok_ok ? (uint32_t)mrow[g] : 1u) : 0u;
+            wv_[e] = g < g1 && tid < 2 * TILE_N ? (uint32_t)wrow[(size_t)g * 64] : 0u;
         }
         uint32_t xw[3][4], ww[3][4];
 #pragma unroll
@@ -878,7 +883,7 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
             digits4(xv + 4 * q, xw[0][q], xw[1][q], xw[2][q]);
             digits4(wv_ + 4 * q, ww[0][q], ww[1][q], ww[2][q]);
         }
-        if (k0 > 0) __syncthreads();          // the previous chunk's digit reads are done
+        if (k0 > g0) __syncthreads();         // the previous chunk's digit reads are done
 #pragma unroll
         for (int d = 0; d < 3; d++) {
             *reinterpret_cast<uint4*>(xd + (d * P2_BM + sl) * 32 + sh) = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
@@ -920,6 +925,37 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
     }
 
     P2_TR(63, 2);
+    // ---- K-slices: every slice stores its exact int64 sums into its own plane of `part` (agent-scope stores,
+    // coherent across the XCDs' L2s), waits until they are performed and counts itself in cnt[tile]; the slice
+    // that arrives last adds the other planes and runs the epilogue, then resets the counter
+    if (KS > 1) {
+        const size_t npad = (size_t)nbn * TILE_N, mpad = (size_t)nbt * P2_BM;
+        const int tcount = tb * nbn + nb;
+        const int tr0 = t0 + wv * 32 + 4 * lh;                   // token of register 0; register r adds 8 (r / 4) + r % 4
+        auto at = [&](int k, int j, int r) __attribute__((always_inline)) {
+            return part + ((size_t)k * mpad + tr0 + 8 * (r >> 2) + (r & 3)) * npad + n0 + 32 * j + l32;
+        };
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                __hip_atomic_store(at(ks, j, r), (long long)U[j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);             // this wave's stores have been performed
+        __syncthreads();
+        if (tid == 0)
+            last_s = __hip_atomic_fetch_add(cnt + tcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);
+        __syncthreads();
+        if (!last_s) return;
+        for (int k = 0; k < KS; k++) {
+            if (k == ks) continue;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    U[j][r] += (unsigned long long)__hip_atomic_load(at(k, j, r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (tid == 0) __hip_atomic_store(cnt + tcount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // ---- epilogue: y = (f32(acc) * c[n]) * sx[t]; a tile routed whole to one plain output stores unchecked
     const bool full = t0 + P2_BM <= M && n0 + TILE_N <= N && out.nparts <= 1;
 #pragma unroll
@@ -1126,9 +1162,19 @@ void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, cons
     DET_CHECK(hipGetLastError());
 }
 
-// K-slice partial sums of k_decode_ms: part[KS][MT][Npad] int64 (each slice stores its own plane, so no zeroing)
-long long* g_part_ms = nullptr;
-size_t g_part_ms_cap = 0;
+// K-slice partial sums of k_decode_ms and k_prefill2: part[KS][tokens][Npad] int64 (each slice stores its own
+// plane, so nothing needs zeroing); library-owned, grown on demand
+long long* g_part_ks = nullptr;
+size_t g_part_ks_cap = 0;
+long long* partial_buffer(size_t elems, hipStream_t st) {
+    if (elems > g_part_ks_cap) {
+        DET_CHECK(hipStreamSynchronize(st));     // earlier launches may still use the old buffer
+        if (g_part_ks) DET_CHECK(hipFree(g_part_ks));
+        g_part_ks_cap = std::max(elems, (size_t)1 << 20);
+        DET_CHECK(hipMalloc(&g_part_ks, g_part_ks_cap * 8));
+    }
+    return g_part_ks;
+}
 
 template <int BITS, int TS>
 void launch_decode_ms(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
@@ -1150,15 +1196,8 @@ void launch_decode_ms(const det_qlinear& L, const int8_t* xq, const float* sx, c
     long long* part = nullptr;
     unsigned int* cnt = nullptr;
     if (KS > 1) {
-        const size_t need = (size_t)KS * MT * T * TILE_N;
-        if (need > g_part_ms_cap) {
-            DET_CHECK(hipStreamSynchronize(st));
-            if (g_part_ms) DET_CHECK(hipFree(g_part_ms));
-            g_part_ms_cap = std::max(need, (size_t)1 << 20);
-            DET_CHECK(hipMalloc(&g_part_ms, g_part_ms_cap * 8));
-        }
+        part = partial_buffer((size_t)KS * MT * T * TILE_N, st);
         decode_buffers(0, (size_t)T, st);        // arrival counters (shared with k_decode: zero between calls)
-        part = g_part_ms;
         cnt = g_cnt;
     }
     const int NS = (gs + 31) & ~31;
@@ -1179,7 +1218,21 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         else launch_decode_ms<BITS, 2>(L, xq, sx, mx, M, y, st);
     } else {
         const int nbn = (L.N + TILE_N - 1) / TILE_N, nbt = (M + P2_BM - 1) / P2_BM;
-        k_prefill2<BITS><<<nbn * nbt, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt);
+        // K-slices when the tiles leave CUs idle: up to 1.5 workgroups per CU, each slice at least 16 groups (the
+        // combine costs about as much as a few groups)
+        const int G = L.K / GROUP, tiles = nbn * nbt, cus = g_decode_waves / 8;
+        int KS = 1;
+        if (2 * tiles < 3 * cus) KS = std::max(1, std::min((3 * cus + 2 * tiles - 1) / (2 * tiles), G / 16));
+        const int gs = (G + KS - 1) / KS;
+        KS = (G + gs - 1) / gs;                  // no empty slices
+        long long* part = nullptr;
+        unsigned int* cnt = nullptr;
+        if (KS > 1) {
+            part = partial_buffer((size_t)KS * nbt * P2_BM * nbn * TILE_N, st);
+            decode_buffers(0, (size_t)tiles, st);
+            cnt = g_cnt;
+        }
+        k_prefill2<BITS><<<tiles * KS, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt, KS, part, cnt);
         DET_CHECK(hipGetLastError());
     }
 }
