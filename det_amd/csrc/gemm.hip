@@ -19,7 +19,8 @@
 //       the buffer unit; one v_mfma_i32_32x32x32_i8 per 32 codes and token set; group scaling with two VALU ops per
 //       output (biased partials, bias removed by digit-product MFMAs once per workgroup).
 //   k_prefill2<BITS> (M > 64): 128-token x 64-row workgroup tiles, three workgroups per CU, activations copied
-//       global -> LDS by the buffer unit, the same biased scaling.
+//       global -> LDS by the buffer unit, W4/W6 codes unpacked from registers a group ahead into a double-buffered
+//       tile (one barrier per group), the same biased scaling.
 #include <string.h>
 #include <algorithm>
 #include "common.h"
@@ -690,13 +691,13 @@ __device__ unsigned long long g_trace2[4 * 4 * 64 * 8];
 // Workgroup tile 128 tokens x 64 rows (one weight tile), 4 waves of 32 tokens x 64 rows; up to three workgroups per
 // CU (<= 168 VGPRs, <= 50 KB LDS), so a CU holds 12 waves whose MFMA chains, scaling and copy waits interleave.
 // Per 128-group g (one round):
-//   - every wave waits for its own copies of round g and stages its multiplier; barrier;
-//   - W4/W6: the packed codes (single staging buffer) are unpacked into the signed tile Bs, one 32-code block per
-//     lane (wave = block, lane = row); barrier.  W8: the MFMA reads its B operand straight from the staging buffer
-//     (tile layout: plane c holds bytes 16 c .. 16 c + 15 of the 64 rows), which is double buffered;
-//   - the copies of group g + 1 are issued by the buffer unit into LDS in two runs per wave, the activations right
-//     after the first barrier and the codes after the second (so each run's M0 change finds the previous run long
-//     issued), the multipliers into a register;
+//   - every wave waits for its own copies and loads of round g and stages its multiplier; one barrier;
+//   - W4/W6: each lane unpacks its 32-code block of group g + 1 (wave = block, lane = row; the packed bytes were
+//     loaded into registers during the previous round) into the other half of the double-buffered signed tile Bs.
+//     W8 needs no unpack: the MFMA reads its B operand straight from a double-buffered copy of the codes (tile
+//     layout: plane c holds bytes 16 c .. 16 c + 15 of the 64 rows);
+//   - the activations of group g + 1 are copied by the buffer unit into LDS (W8 also its codes), the multipliers
+//     loaded into a register, W4/W6 group g + 2's packed block into registers;
 //   - 8 v_mfma_i32_32x32x32_i8 (two chains from the bias B) and the scaling U += (p + B) * (m * mx).
 // Group scaling with two VALU ops per (token, row, group): each group's MFMA chain starts from a constant
 // accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
@@ -713,10 +714,10 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
                                                       long long* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int NC = group_bytes(BITS) / 16;                 // 1 KB planes per tile-group
     constexpr int WB = NC * 1024;
-    constexpr int NSTAGE = BITS == 8 ? 2 : 1;                  // W8 computes from the staging buffer
+    constexpr bool W8 = BITS == 8;    // W8: codes copied into a double-buffered staging tile the MFMA reads directly
     __shared__ __attribute__((aligned(16))) int8_t As[2][P2_BM * 128];
-    __shared__ __attribute__((aligned(16))) int8_t Bp[NSTAGE][WB];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[BITS == 8 ? 16 : TILE_N * 128];
+    __shared__ __attribute__((aligned(16))) int8_t Bp[2][W8 ? WB : 16];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[2][W8 ? 16 : TILE_N * 128];   // W4/W6: unpacked tiles
     __shared__ __attribute__((aligned(16))) uint32_t mxs[2][P2_BM];   // mx of the tile's tokens, per buffer
     __shared__ uint16_t mss[2][TILE_N];                                // m of the tile's rows, per buffer
     __shared__ unsigned int last_s;
@@ -754,32 +755,68 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
                                                   M > 8 * i ? (M - 8 * i) * K + 1024 * i : 0, 0x00020000);
     const uint32_t a_vo = (uint32_t)(t0 + wv * 32 + (lane >> 3)) * (uint32_t)K + (uint32_t)(((lane & 7) ^ (lane >> 4)) * 16);
     const uint32_t a_vo1 = a_vo ^ 64u;
-    // codes: the tile-group is WB contiguous bytes; wave w copies planes PW w .. PW w + PW - 1
-    constexpr int PW = BITS == 4 ? 1 : 2;
-    const bool w_copies = wvu * PW < NC;
+    // W8 codes: the tile-group is WB contiguous bytes; wave w copies planes 2 w, 2 w + 1
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)(wq + (size_t)nb * G * WB), (short)0, G * WB, 0x00020000);
     const uint32_t w_vo[2] = {(uint32_t)lane * 16, (uint32_t)lane * 16};
-    // multipliers: thread tid < 128 loads mx of token t0 + tid, 128 <= tid < 192 m of row tid - 128
+    // W4/W6 codes: wave w = block b (32 codes), lane = row r: bytes BPL b .. BPL b + BPL - 1 of the row's group,
+    // loaded into registers two groups ahead of their use (W4 plane b; W6 16 bytes of plane 3 (b / 2) + 2 (b % 2)
+    // and 8 bytes of plane 3 (b / 2) + 1 at byte 8 (b % 2), the odd blocks' low words starting with the latter)
+    const uint8_t* wcodes = wq + (size_t)nb * G * WB + lane * 16;
+    uint32_t qn[6];
+    auto load_w = [&](int g) __attribute__((always_inline)) {
+        const uint8_t* p = wcodes + (size_t)g * WB;
+        if constexpr (BITS == 4) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p + wvu * 1024);
+            qn[0] = v.x; qn[1] = v.y; qn[2] = v.z; qn[3] = v.w;
+        } else if constexpr (BITS == 6) {
+            const int pp = 3 * (wvu >> 1);
+            const uint4 v = *reinterpret_cast<const uint4*>(p + (pp + 2 * (wvu & 1)) * 1024);
+            const uint2 w = *reinterpret_cast<const uint2*>(p + (pp + 1) * 1024 + 8 * (wvu & 1));
+            qn[0] = v.x; qn[1] = v.y; qn[2] = v.z; qn[3] = v.w; qn[4] = w.x; qn[5] = w.y;
+        }
+    };
+    // unpack the registers' block into the signed tile bs (row lane, chunks 2 b and 2 b + 1); the W6 reorder of odd
+    // blocks happens here, not at the load, so no wait for the load is placed early
+    auto unpack_to = [&](int8_t* bs) __attribute__((always_inline)) {
+        uint32_t o[8];
+        if constexpr (BITS == 6) {
+            const bool odd = wvu & 1;
+            const uint32_t w6[6] = {odd ? qn[4] : qn[0], odd ? qn[5] : qn[1], odd ? qn[0] : qn[2],
+                                    odd ? qn[1] : qn[3], odd ? qn[2] : qn[4], odd ? qn[3] : qn[5]};
+            block_signed<6>(w6, o);
+        } else {
+            block_signed<W8 ? 4 : BITS>(qn, o);
+        }
+        *reinterpret_cast<uint4*>(bs + swz(lane, 2 * wvu)) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4*>(bs + swz(lane, 2 * wvu + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
+    };
+    // multipliers: thread tid < 128 loads mx[t0 + tid][g] (1 for tokens past M or without mx), 128 <= tid < 192
+    // m[tile][g][tid - 128], by plain zero-extending loads (a 16-bit buffer load's result needs a mask, for which
+    // the compiler can wait at once)
     const bool xm = tid < P2_BM, wm_ = tid >= P2_BM && tid < P2_BM + TILE_N;
-    const __amdgpu_buffer_rsrc_t sr_x = __builtin_amdgcn_make_buffer_rsrc((void*)mx, (short)0, mx ? M * G * 2 : 0, 0x00020000);
-    const __amdgpu_buffer_rsrc_t sr_w = __builtin_amdgcn_make_buffer_rsrc((void*)ms, (short)0, (nb + 1) * G * 128, 0x00020000);
-    const uint32_t s_vo = xm ? (uint32_t)(t0 + tid) * (uint32_t)G * 2 : (uint32_t)(nb * G * 64 + (tid - P2_BM)) * 2;
     const bool x_one = xm && !(mx && t0 + tid < M);
+    const bool s_load = (xm && !x_one) || wm_;
+    const uint16_t* s_ptr = xm ? (x_one ? ms : mx + (size_t)(t0 + tid) * G) : ms + (size_t)nb * G * 64 + (wm_ ? tid - P2_BM : 0);
+    const int s_stride = xm ? 1 : 64;
     uint32_t sreg = 1;
 
     auto issue_a = [&](int g) __attribute__((always_inline)) {
         dma16_run4x(xr, a_vo, a_vo1, g * GROUP, As[g & 1] + wvu * 4096);
     };
-    auto issue_w = [&](int g) __attribute__((always_inline)) {
-        if (w_copies) dma16_run<PW>(wr, w_vo, g * WB + wvu * PW * 1024, Bp[NSTAGE == 2 ? (g & 1) : 0] + wvu * PW * 1024);
-        // uniform branches: one resource per wave
-        if (wvu < 2) sreg = __builtin_amdgcn_raw_buffer_load_b16(sr_x, s_vo, g * 2, 0);
-        else if (wvu == 2) sreg = __builtin_amdgcn_raw_buffer_load_b16(sr_w, s_vo, g * 128, 0);
+    auto issue_s = [&](int g) __attribute__((always_inline)) {
+        if (s_load) sreg = s_ptr[(size_t)g * s_stride];
     };
 
     P2_TR(63, 0);
     issue_a(g0);
-    issue_w(g0);
+    issue_s(g0);
+    if constexpr (W8) {
+        dma16_run<2>(wr, w_vo, g0 * WB + wvu * 2048, Bp[g0 & 1] + wvu * 2048);
+    } else {
+        load_w(g0);
+        unpack_to(Bs[g0 & 1]);
+        if (g0 + 1 < g1) load_w(g0 + 1);
+    }
     for (int g = g0; g < g1; g++) {
         const int par = g & 1;
         P2_TR(g, 0);
@@ -787,36 +824,21 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
         P2_TR(g, 1);
         if (xm) mxs[par][tid] = x_one ? 1u : sreg;
         else if (wm_) mss[par][tid - P2_BM] = (uint16_t)sreg;
-        __syncthreads();                      // group g's copies have landed; group g - 1's compute is done
-        if (g + 1 < g1) issue_a(g + 1);       // As[(g + 1) % 2] was last read by group g - 1's compute
+        __syncthreads();                      // group g's copies and unpacked codes are in place; group g - 1's
+                                              // compute is done, so the other buffers are free
         P2_TR(g, 2);
-        if constexpr (BITS != 8) {
-            // unpack: wave = block b, lane = row; block b is bytes 8 NC/2... of the row's packed group
-            const int r = lane, b = wvu;
-            uint32_t q[6];
-            if constexpr (BITS == 6) {
-                const int8_t* p0 = Bp[0] + (3 * (b >> 1)) * 1024 + r * 16;
-                if ((b & 1) == 0) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(p0);
-                    const uint2 w = *reinterpret_cast<const uint2*>(p0 + 1024);
-                    q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w; q[4] = w.x; q[5] = w.y;
-                } else {
-                    const uint2 w = *reinterpret_cast<const uint2*>(p0 + 1024 + 8);
-                    const uint4 v = *reinterpret_cast<const uint4*>(p0 + 2048);
-                    q[0] = w.x; q[1] = w.y; q[2] = v.x; q[3] = v.y; q[4] = v.z; q[5] = v.w;
-                }
-            } else {
-                const uint4 v = *reinterpret_cast<const uint4*>(Bp[0] + b * 1024 + r * 16);
-                q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
-            }
-            uint32_t o[8];
-            block_signed<BITS>(q, o);
-            *reinterpret_cast<uint4*>(Bs + swz(r, 2 * b)) = make_uint4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<uint4*>(Bs + swz(r, 2 * b + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
-            __syncthreads();                  // Bs complete; the staging buffer is free again
+        if constexpr (!W8) {
+            // group g + 1's codes (loaded during the previous round) into the other tile, before any new load is
+            // issued (so the wait for those registers finds nothing newer outstanding)
+            if (g + 1 < g1) unpack_to(Bs[(g + 1) & 1]);
         }
         P2_TR(g, 3);
-        if (g + 1 < g1) issue_w(g + 1);       // W8: Bp[(g + 1) % 2] was last read by group g - 1's compute
+        if (g + 1 < g1) {
+            issue_a(g + 1);
+            issue_s(g + 1);
+            if constexpr (W8) dma16_run<2>(wr, w_vo, (g + 1) * WB + wvu * 2048, Bp[(g + 1) & 1] + wvu * 2048);
+            else if (g + 2 < g1) load_w(g + 2);
+        }
         P2_TR(g, 4);
         // MFMA over group g and scaling into U
         const int8_t* Ab = As[par];
@@ -830,8 +852,8 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
                 b0 = *reinterpret_cast<const v4i*>(Bb + l32 * 16);
                 b1 = *reinterpret_cast<const v4i*>(Bb + (32 + l32) * 16);
             } else {
-                b0 = *reinterpret_cast<const v4i*>(Bs + swz(l32, 2 * s + lh));
-                b1 = *reinterpret_cast<const v4i*>(Bs + swz(32 + l32, 2 * s + lh));
+                b0 = *reinterpret_cast<const v4i*>(Bs[par] + swz(l32, 2 * s + lh));
+                b1 = *reinterpret_cast<const v4i*>(Bs[par] + swz(32 + l32, 2 * s + lh));
             }
             d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, s == 0 ? biasv : d[0], 0, 0, 0);
             d[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, s == 0 ? biasv : d[1], 0, 0, 0);

@@ -37,7 +37,6 @@ def prefill2_copies(N, K, M, bits):
     T = 2 * ((N + 127) // 128)
     nbn, nbt = (N + TILE_N - 1) // TILE_N, (M + P2_BM - 1) // P2_BM
     nc, wb = NC[bits], NC[bits] * 1024
-    pw = 1 if bits == 4 else 2
     lane = np.arange(64)
     xq_size, wq_size, mx_size, ms_size = M * K, T * G * wb, M * G * 2, T * G * TILE_N * 2
     for nb, tb, g, wv in itertools.product(range(nbn), range(nbt), sorted({0, G // 2, G - 1}), range(4)):
@@ -52,12 +51,15 @@ def prefill2_copies(N, K, M, bits):
             check_in(lo, hi, xq_size, f'prefill2 A copy {i} N={N} K={K} M={M} tb={tb} wv={wv} g={g}')
             lds = 4096 * wv + 1024 * i + 16 * lane
             assert lds.max() + 16 <= P2_BM * 128
-        # codes: resource wq + nb G WB of size G WB, per-lane offset 16 lane, copies of the wave's planes
-        if wv * pw < nc:
-            for i in range(pw):
-                lo, hi = reached(nb * G * wb, 16 * lane, 1024 * i, g * wb + wv * pw * 1024, G * wb)
+        # W8 codes: resource wq + nb G WB of size G WB, per-lane offset 16 lane, the wave's planes 2 wv, 2 wv + 1;
+        # W4/W6 codes: plain loads of block wv of row lane, two groups ahead (into registers)
+        if bits == 8:
+            for i in range(2):
+                lo, hi = reached(nb * G * wb, 16 * lane, 1024 * i, g * wb + wv * 2048, G * wb)
                 check_in(lo, hi, wq_size, f'prefill2 W copy N={N} K={K}')
-                assert wv * pw * 1024 + 1024 * i + 16 * 63 + 16 <= wb
+                assert wv * 2048 + 1024 * i + 16 * 63 + 16 <= wb
+        else:
+            check_code_loads(bits, nb * G * wb + g * wb + lane * 16, np.full(64, wv), wq_size)
         # multipliers: mx through a resource of size M G 2 at per-lane offset (t0 + tid) G 2, scalar offset 2 g;
         # m through a resource of size (nb + 1) G 128 at (nb G 64 + row) 2, scalar offset 128 g
         tid = 64 * wv + lane
@@ -67,6 +69,31 @@ def prefill2_copies(N, K, M, bits):
         elif wv == 2:
             lo, hi = reached(0, (nb * G * 64 + (tid - P2_BM)) * 2, 0, 128 * g, (nb + 1) * G * 128, 2)
             check_in(lo, hi, ms_size, 'prefill2 m load')
+
+
+def check_code_loads(bits, base, blk, wq_size):
+    """Per-lane loads of one 32-code block blk of a row whose tile-group slot starts at base (plane c of the group
+    at + 1024 c): in bounds, aligned, and exactly bytes BPL blk .. BPL blk + BPL - 1 of the row's group, in the
+    word order the unpack takes (W6 odd blocks: the 8-byte load's words first)."""
+    bpl = {4: 16, 6: 24, 8: 32}[bits]
+    if bits == 4:
+        spans = [(blk * 1024, 16)]
+    elif bits == 8:
+        spans = [(2 * blk * 1024, 16), ((2 * blk + 1) * 1024, 16)]
+    else:   # v (words 0-3), w (words 4-5)
+        pp = 3 * (blk >> 1)
+        spans = [((pp + 2 * (blk & 1)) * 1024, 16), ((pp + 1) * 1024 + 8 * (blk & 1), 8)]
+    for rel, n in spans:
+        off = base + rel
+        assert off.min() >= 0 and (off + n).max() <= wq_size, f'code load W{bits}'
+        assert (off % n == 0).all(), 'unaligned code load'
+    # row-group byte of each loaded byte: plane c byte j is byte 16 c + j
+    grp = [16 * (rel // 1024) + rel % 1024 + np.arange(n)[:, None] for rel, n in spans]
+    if bits == 6:
+        words = np.where((blk & 1).astype(bool), np.concatenate([grp[1], grp[0]]), np.concatenate(grp))
+    else:
+        words = np.concatenate(grp)
+    assert (words == bpl * blk + np.arange(bpl)[:, None]).all(), 'lane block bytes'
 
 
 def decode_ms_copies(N, K, M, ts):
