@@ -372,6 +372,17 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
     }
 }
 
+// int64 -> fp32 (round to nearest even) for the epilogues: |v| < 2^52 is exact as a double (high word times 2^32
+// plus the low word, one fma), and the double -> float conversion then rounds once; larger magnitudes take
+// i64_to_f.
+__device__ __forceinline__ float i64_to_f_fast(long long v) {
+    const int hi = (int)(v >> 32);
+    if ((uint32_t)(hi + (1 << 20)) < (1u << 21)) {       // -2^52 <= v < 2^52
+        const double d = __builtin_fma((double)hi, 4294967296.0, (double)(uint32_t)v);
+        return (float)d;
+    }
+    return i64_to_f(v);
+}
 // start value of every MFMA chain in the biased scaling: |p| <= 128 * 127 * 128 < 2^21, so p + B >= 0
 constexpr uint32_t PF_BIAS = 1u << 21;
 // a * b for a, b < 2^16 (m and mx).  Inline asm: the compiler turns __umul24 of operands it cannot bound into an
@@ -434,6 +445,13 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
     __shared__ unsigned int last_s;
     const int lane = threadIdx.x & 63, W = blockDim.x >> 6, P = W >> 1;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // token block blockIdx.y: tokens t0 .. t0 + MT - 1 (the launch has ceil(M / MT) of them); from here on xq, sx,
+    // mx and M describe the block's own tokens, and only the output rows and the K-slice buffers see t0
+    const int tbk = blockIdx.y, t0 = tbk * MT;
+    xq += (size_t)t0 * K;
+    sx += t0;
+    if (mx) mx += (size_t)t0 * (K / GROUP);
+    M -= t0;
     const int pr = wv >> 1, hf = wv & 1;        // pair and row half of this wave
     const int e = lane >> 5, l32 = lane & 31, row = 32 * hf + l32;
     const int tile = blockIdx.x / KS, ks = blockIdx.x - tile * KS;
@@ -570,12 +588,12 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
             const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[0], z, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                // d4 < 2^13, d3 < 2^19, d2, d1 < 2^20, d0 < 2^19: the top part fits int32, the rest int64
-                const int hi = (d4[r] << 7) + d3[r];                                     // < 2^21
-                long long S = ((long long)hi << 7) + d2[r];
-                S = (S << 7) + d1[r];
-                S = (S << 7) + d0[r];
-                U[t][r] -= (unsigned long long)S << 21;
+                // d4 < 2^9, d3 < 2^15, d2, d1 < 2^20, d0 < 2^19 (32 slots): S = hi 2^14 + lo with
+                // hi = (d4 2^7 + d3) 2^7 + d2 < 2^25 and lo = d1 2^7 + d0 < 2^28, one v_mad_u64_u32
+                const uint32_t hi = (((uint32_t)d4[r] << 7) + (uint32_t)d3[r] << 7) + (uint32_t)d2[r];
+                const uint32_t lo = ((uint32_t)d1[r] << 7) + (uint32_t)d0[r];
+                const unsigned long long S = (unsigned long long)hi * 16384u + lo;
+                U[t][r] -= S << 21;
             }
         }
     }
@@ -612,6 +630,8 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
     }
     if (KS > 1) {
         const size_t npad = (size_t)(gridDim.x / KS) * TILE_N;
+        part += (size_t)tbk * KS * MT * npad;                  // this token block's planes
+        cnt += (size_t)tbk * (gridDim.x / KS);                 // and counters
         long long* mine = part + (size_t)ks * MT * npad;
 #pragma unroll
         for (int i = 0; i < EI; i++) {
@@ -642,20 +662,20 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
 #pragma unroll
     for (int i = 0; i < EI; i++) {
         const int t = wv + W * i;
-        f[i] = (i64_to_f(v[i]) * cn) * sxs_s[t < MT ? t : 0];
+        f[i] = (i64_to_f_fast(v[i]) * cn) * sxs_s[t < MT ? t : 0];
     }
     if (n >= N) return;
     if (!out.acc && out.nparts <= 1) {
 #pragma unroll
         for (int i = 0; i < EI; i++) {
             const int t = wv + W * i;
-            if (t < mt) out.y[(size_t)t * N + n] = f[i];
+            if (t < mt) out.y[(size_t)(t0 + t) * N + n] = f[i];
         }
     } else {
 #pragma unroll
         for (int i = 0; i < EI; i++) {
             const int t = wv + W * i;
-            if (t < mt) out.store(N, t, n, f[i]);
+            if (t < mt) out.store(N, t0 + t, n, f[i]);
         }
     }
     DMS_TR(63, 3);
@@ -668,17 +688,6 @@ constexpr int P2_BM = 128;        // tokens per workgroup of k_prefill2
 // (chunk position c ^ ((r / 2) % 8): the 16 rows that one LDS cycle serves fall on 16 distinct 16-byte bank slots)
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
-// int64 -> fp32 (round to nearest even) for the epilogues: |v| < 2^52 is exact as a double (high word times 2^32
-// plus the low word, one fma), and the double -> float conversion then rounds once; larger magnitudes take
-// i64_to_f.
-__device__ __forceinline__ float i64_to_f_fast(long long v) {
-    const int hi = (int)(v >> 32);
-    if ((uint32_t)(hi + (1 << 20)) < (1u << 21)) {       // -2^52 <= v < 2^52
-        const double d = __builtin_fma((double)hi, 4294967296.0, (double)(uint32_t)v);
-        return (float)d;
-    }
-    return i64_to_f(v);
-}
 #ifdef P2_TRACE
 __device__ unsigned long long g_trace2[4 * 4 * 64 * 8];
 #define P2_TR(it, slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
@@ -1198,33 +1207,39 @@ long long* partial_buffer(size_t elems, hipStream_t st) {
     return g_part_ks;
 }
 
+// K-slices of k_decode_ms for `units` (tile, token block) pairs: until every CU has a workgroup, each slice keeping
+// at least 16 groups (the slices' combine costs about as much as a few rounds) and at most DMS_MAXSLOT
+int dms_slices(int units, int G) {
+    const int cus = g_decode_waves / 8;
+    int KS = units >= cus ? 1 : std::max(1, std::min((cus + units - 1) / units, G / 16));
+    KS = std::max(KS, (G + DMS_MAXSLOT - 1) / DMS_MAXSLOT);
+    const int gs = (G + KS - 1) / KS;
+    return (G + gs - 1) / gs;                    // no empty slices
+}
+
 template <int BITS, int TS>
 void launch_decode_ms(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
     constexpr int MT = 32 * TS;
     const int G = L.K / GROUP;
     const int T = (L.N + TILE_N - 1) / TILE_N;
+    const int NB = (M + MT - 1) / MT;            // token blocks (grid y)
+    const int units = T * NB;
     const int cus = g_decode_waves / 8;
-    // K-slices until every CU has a workgroup (the second workgroup a CU holds overlaps the first's prologue and
-    // epilogue), each slice at most DMS_MAXSLOT groups
-    // K-slices until every CU has a workgroup, each slice keeping at least 16 groups (the slices' combine costs
-    // about as much as a few rounds) and at most DMS_MAXSLOT
-    int KS = T >= cus ? 1 : std::max(1, std::min((cus + T - 1) / T, G / 16));
-    KS = std::max(KS, (G + DMS_MAXSLOT - 1) / DMS_MAXSLOT);
+    const int KS = dms_slices(units, G);
     const int gs = (G + KS - 1) / KS;
-    KS = (G + gs - 1) / gs;                      // no empty slices
     // four pairs when every workgroup has a CU of its own, else two (two workgroups share a CU, one's prologue and
     // epilogue overlapping the other's rounds)
-    const int P = std::min(T * KS <= cus ? DMS_MAXP : 2, gs);
+    const int P = std::min(units * KS <= cus ? DMS_MAXP : 2, gs);
     long long* part = nullptr;
     unsigned int* cnt = nullptr;
     if (KS > 1) {
-        part = partial_buffer((size_t)KS * MT * T * TILE_N, st);
-        decode_buffers(0, (size_t)T, st);        // arrival counters (shared with k_decode: zero between calls)
+        part = partial_buffer((size_t)NB * KS * MT * T * TILE_N, st);
+        decode_buffers(0, (size_t)units, st);    // arrival counters (shared with k_decode: zero between calls)
         cnt = g_cnt;
     }
     const int NS = (gs + 31) & ~31;
     const size_t lds = std::max((size_t)2 * P * MT * 128, (size_t)MT * TILE_N * 8) + (size_t)3 * (64 + MT) * NS;
-    k_decode_ms<BITS, TS><<<T * KS, 128 * P, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
+    k_decode_ms<BITS, TS><<<dim3(T * KS, NB), 128 * P, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
     DET_CHECK(hipGetLastError());
 }
 
@@ -1236,7 +1251,11 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         else if (M <= 8) launch_decode<BITS, 8>(L, xq, sx, mx, M, y, st);
         else launch_decode<BITS, 16>(L, xq, sx, mx, M, y, st);
     } else if (M <= 64) {
-        if (M <= 32) launch_decode_ms<BITS, 1>(L, xq, sx, mx, M, y, st);
+        // 33..64 tokens: one 64-token block per tile, or two 32-token blocks (each unpacking the tile's codes for
+        // half the tokens) when that gives more workgroups than the K-slices of the 64-token blocks do
+        const int T = (L.N + TILE_N - 1) / TILE_N, G = L.K / GROUP;
+        const bool split = M > 32 && 2 * T * dms_slices(2 * T, G) > T * dms_slices(T, G);
+        if (M <= 32 || split) launch_decode_ms<BITS, 1>(L, xq, sx, mx, M, y, st);
         else launch_decode_ms<BITS, 2>(L, xq, sx, mx, M, y, st);
     } else {
         const int nbn = (L.N + TILE_N - 1) / TILE_N, nbt = (M + P2_BM - 1) / P2_BM;

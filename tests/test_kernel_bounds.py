@@ -96,21 +96,37 @@ def check_code_loads(bits, base, blk, wq_size):
     assert (words == bpl * blk + np.arange(bpl)[:, None]).all(), 'lane block bytes'
 
 
-def decode_ms_copies(N, K, M, ts):
+def decode_ms_copies(N, K, M, ts, KS=1):
+    """k_decode_ms: token block y (tokens t0 = 32 ts y ..) copies through a resource based at xq + t0 K whose range
+    is its own M - t0 rows; K-slice planes and counters are indexed by the block as well."""
     G = K // GROUP
     mt = 32 * ts
     ncp = mt // 16
+    T = (N + TILE_N - 1) // TILE_N
+    NB = (M + mt - 1) // mt
     lane = np.arange(64)
-    for hf, g in itertools.product(range(2), sorted({0, G - 1})):
-        R = (mt // 2) * hf + 8 * np.arange(ncp)[:, None] + (lane >> 3)[None, :]
-        xvo = R * K + (((lane & 7)[None, :] ^ ((R >> 1) & 7)) * 16) - 1024 * (np.arange(ncp)[:, None] & 3)
-        for c0 in range(0, ncp, 4):
-            n = 4 if ncp - c0 >= 4 else 2
-            for j in range(n):
-                lo, hi = reached(0, xvo[c0 + j], 1024 * j, g * GROUP, M * K)
-                check_in(lo, hi, M * K, f'decode_ms copy N={N} K={K} M={M} hf={hf}')
-                lds = (mt // 2) * hf * 128 + c0 * 1024 + 1024 * j + 16 * lane
-                assert lds.max() + 16 <= mt * 128
+    for tbk in range(NB):
+        t0, Mb = tbk * mt, M - tbk * mt
+        assert Mb >= 1
+        for hf, g in itertools.product(range(2), sorted({0, G - 1})):
+            R = (mt // 2) * hf + 8 * np.arange(ncp)[:, None] + (lane >> 3)[None, :]
+            xvo = R * K + (((lane & 7)[None, :] ^ ((R >> 1) & 7)) * 16) - 1024 * (np.arange(ncp)[:, None] & 3)
+            for c0 in range(0, ncp, 4):
+                n = 4 if ncp - c0 >= 4 else 2
+                for j in range(n):
+                    lo, hi = reached(t0 * K, xvo[c0 + j], 1024 * j, g * GROUP, Mb * K)
+                    check_in(lo, hi, M * K, f'decode_ms copy N={N} K={K} M={M} block={tbk} hf={hf}')
+                    lds = (mt // 2) * hf * 128 + c0 * 1024 + 1024 * j + 16 * lane
+                    assert lds.max() + 16 <= mt * 128
+        # token multipliers mx[t0 + lane][g] for lane < min(M - t0, MT); sx[t0 + min(lane, M - t0 - 1)]
+        tl = lane[lane < min(Mb, mt)]
+        assert ((t0 + tl) * G + G - 1).max() < M * G and t0 + min(63, Mb - 1) < M
+        # K-slice planes part[NB][KS][MT][T * 64] and counters cnt[NB][T]
+        npad = T * TILE_N
+        for ks in range(KS):
+            idx = ((tbk * KS + ks) * mt + np.arange(min(Mb, mt))[:, None]) * npad + np.arange(npad)
+            assert idx.max() < NB * KS * mt * T * TILE_N
+        assert tbk * T + T - 1 < NB * T
 
 
 SHAPES = [(640, 2560), (9728, 2560), (2560, 9728), (200, 384), (48, 128), (17408, 5120), (5120, 17408)]
@@ -125,8 +141,8 @@ def test_prefill2_copies_in_bounds(N, K, bits):
 
 @pytest.mark.parametrize('N,K', SHAPES)
 def test_decode_ms_copies_in_bounds(N, K):
-    for M, ts in ((17, 1), (20, 1), (32, 1), (33, 2), (50, 2), (64, 2)):
-        decode_ms_copies(N, K, M, ts)
+    for M, ts in ((17, 1), (20, 1), (32, 1), (33, 2), (50, 2), (64, 2), (33, 1), (50, 1), (64, 1)):
+        decode_ms_copies(N, K, M, ts, KS=1 if K < 4096 else 3)
 
 
 def test_scalar_offset_is_not_checked():
