@@ -13,6 +13,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, 'libdet_oracle.so')
 SRC = os.path.join(HERE, 'det_oracle.c')
+MIXER_SRC = os.path.join(HERE, 'mixer_oracle.c')
 
 CFLAGS = ['-O2', '-fPIC', '-shared', '-ffp-contract=off', '-fno-fast-math', '-fopenmp', '-Wall']
 
@@ -31,7 +32,7 @@ def build():
             subprocess.check_call(['gcc', '-O3', '-fPIC', '-fopenmp', '-Wall', '-c', f'-DXVNNI={vnni}'] + isa +
                                   ['-o', o, X86_SRC])
             objs.append(o)
-        subprocess.check_call(['gcc'] + CFLAGS + ['-o', LIB_PATH, SRC] + objs + ['-lm'])
+        subprocess.check_call(['gcc'] + CFLAGS + ['-o', LIB_PATH, SRC, MIXER_SRC] + objs + ['-lm'])
 
 
 _lib = None
@@ -63,6 +64,15 @@ def lib():
             'ora_rng_byte': (ctypes.c_uint8, [u64p]), 'ora_rng_below': (ctypes.c_uint64, [u64p, ctypes.c_uint64]),
             'ora_rng_denorm': (f, [u64p]), 'ora_rng_units': (None, [u64p, P, sz]),
             'ora_fake_rows': (None, [u64p, i, i, i, P]), 'ora_acts_x': (None, [u64p, i, i, P]),
+            'ora_rmsnorm': (None, [P, P, f, i, P]),
+            'ora_l2norm': (None, [P, f, i, P]), 'ora_rope': (None, [P, P, P, i]),
+            'ora_quant_v': (None, [P, f, i, P]),
+            'ora_attn_head': (None, [P, f, P, P, P, i, i, i, f, i, P]),
+            'ora_attention': (None, [P, P, P, P, P, P, P, P, P, P, P, P, i, f, i, i, i, i, i, P]),
+            'ora_gdn_conv': (f, [P, P]), 'ora_gdn_decay': (f, [f, f, f]),
+            'ora_gdn_head_step': (None, [P, i, i, P, P, P, f, f, P]),
+            'ora_gdn': (None, [P, P, P, P, P, P, P, P, P, P, f, i, i, i, i, i, P]),
+            'ora_argmax': (i, [P, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
