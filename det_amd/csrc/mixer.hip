@@ -1,0 +1,449 @@
+// The token mixers of det's qwen35 forward and argmax: attention over the int8 / int16 KV cache, the Gated
+// DeltaNet (conv, l2norm, recurrence, gated norm) and argmax.  Semantics are those of the reference backend
+// (crates/det/src/cpu.rs:212-383 over spec/layers.rs, spec/prim.rs:154-190, spec/sample.rs:6-14); the C ABI is
+// det_cuda.h:60-103's (det_attention, det_gdn, det_argmax).
+//
+// Every reduction the spec orders is reproduced in that order: treesum is a balanced tree over the row padded to a
+// power of two (ping-pong LDS levels, or an in-register subtree per lane plus lane shuffles that combine the
+// aligned subtrees in tree order); the attention max is an fmax fold (order-free) and its weighted sums are exact
+// int64 integers (order-free).
+#include "common.h"
+#include "../../include/det_hip.h"
+using namespace det;
+
+namespace {
+
+constexpr int RT = 256;          // threads of the row kernels
+constexpr int KC = 1024;         // keys per chunk of the attention's second pass
+
+__device__ __forceinline__ int p2(int n) { int p = 1; while (p < n) p <<= 1; return p; }
+
+__device__ __forceinline__ float wave_fmax(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmax_spec(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// spec/prim.rs:154-170 treesum of v[0..n) (squared when SQ) over the block; s, t: LDS scratch of p2(n) and
+// p2(n) / 2 floats.  Every thread returns the sum; s and t are free again when it returns.
+template <bool SQ>
+__device__ float block_treesum(const float* v, int n, float* s, float* t) {
+    const int p = p2(n);
+    for (int i = threadIdx.x; i < p; i += blockDim.x) s[i] = i < n ? (SQ ? v[i] * v[i] : v[i]) : 0.0f;
+    for (int w = p >> 1; w >= 1; w >>= 1) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < w; i += blockDim.x) t[i] = s[2 * i] + s[2 * i + 1];
+        float* u = s; s = t; t = u;
+    }
+    __syncthreads();
+    const float r = s[0];
+    __syncthreads();
+    return r;
+}
+
+// order-free max of |v[0..n)| from 0 (spec/prim.rs:193-195); red: LDS of blockDim / 64 floats
+__device__ float block_absmax(const float* v, int n, float* red) {
+    float am = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) am = fmax_spec(am, __builtin_fabsf(v[i]));
+    am = wave_fmax(am);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+    __syncthreads();
+    am = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) am = fmax_spec(am, red[w]);
+    __syncthreads();
+    return am;
+}
+
+// spec/prim.rs:172-181 rmsnorm of x[0..n) in LDS, in place, weights w (global)
+__device__ void block_rmsnorm(float* x, int n, const float* w, float eps, float* s, float* t) {
+    const float ss = block_treesum<true>(x, n, s, t);
+    const float inv = 1.0f / __builtin_sqrtf((ss / (float)n) + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = (x[i] * inv) * w[i];
+    __syncthreads();
+}
+
+// spec/layers.rs:5-13 rope of x in LDS: thread i < half rotates the pair (x[i], x[i + half]), which no other
+// thread touches
+__device__ void block_rope(float* x, const float* cs, const float* sn, int half) {
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const float a = x[i], b = x[i + half];
+        x[i] = (a * cs[i]) - (b * sn[i]);
+        x[i + half] = (b * cs[i]) + (a * sn[i]);
+    }
+    __syncthreads();
+}
+
+// spec/quant.rs:8-16 quant_act_i8 of x[0..n) (LDS) into q; returns s
+__device__ float block_quant_i8(const float* x, int n, int8_t* q, float* red) {
+    const float am = block_absmax(x, n, red);
+    const float s = am == 0.0f ? 1.0f : am / 127.0f;
+    const float inv = 1.0f / s;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) q[i] = (int8_t)clamp_i8(rint_(x[i] * inv));
+    return s;
+}
+
+// ------------------------------------------------------------------ attention (cpu.rs:212-285)
+// One workgroup per (token, kv head): k -> rmsnorm(k_norm) -> rope -> quant_act_i8 into kq / sk at row pos0 + t,
+// v -> quant_v (spec/layers.rs:73-86) into vq.  LDS: x[hd], tree s[p], t[p / 2].
+__global__ void __launch_bounds__(RT) k_attn_kv(const float* __restrict__ k_norm, const float* __restrict__ v_inv_scale,
+                                                int8_t* __restrict__ kq, float* __restrict__ sk, int16_t* __restrict__ vq,
+                                                const float* __restrict__ k, const float* __restrict__ v,
+                                                const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+                                                int half, float eps, int pos0, int n_kv, int hd) {
+    extern __shared__ float lds[];
+    __shared__ float red[RT / 64];
+    float* x = lds;
+    float* s = x + hd;
+    float* t = s + p2(hd);
+    const int tok = blockIdx.x / n_kv, h = blockIdx.x - tok * n_kv, pos = pos0 + tok;
+    const size_t src = ((size_t)tok * n_kv + h) * hd;
+    for (int i = threadIdx.x; i < hd; i += RT) x[i] = k[src + i];
+    __syncthreads();
+    block_rmsnorm(x, hd, k_norm, eps, s, t);
+    block_rope(x, rope_cos + (size_t)pos * half, rope_sin + (size_t)pos * half, half);
+    const size_t row = ((size_t)pos * n_kv + h) * hd;
+    const float sc = block_quant_i8(x, hd, kq + row, red);
+    if (threadIdx.x == 0) sk[(size_t)pos * n_kv + h] = sc;
+    const float vi = v_inv_scale[h];
+    for (int i = threadIdx.x; i < hd; i += RT) {
+        const float r = rint_(v[src + i] * vi);
+        vq[row + i] = (int16_t)(r < -32767.0f ? -32767 : r > 32767.0f ? 32767 : __builtin_isnan(r) ? 0 : (int)r);
+    }
+}
+
+// One workgroup per (token, head): q -> rmsnorm(q_norm) -> rope -> * 1/sqrt(hd) -> quant_act_i8 (qq, sq); keys
+// 0 .. pos of kv head h / rep: s_j = (f32(dot(qq, kq_j)) * sq) * sk_j, mx = fmax fold, pq_j = rint(exp(s_j - mx)
+// * 2^24) as int64, den = sum pq_j, num_i = sum pq_j vq_j[i] (exact, order-free), o_i = ((f32(num_i) / f32(den)) *
+// v_scale) * sigmoid(gate_i) (spec/layers.rs:24-69).  The scores are computed twice (max pass, weight pass).
+// LDS: x[hd] floats, tree s[p], t[p / 2], qq[hd] bytes; static: the chunk's weights, den partials.
+__global__ void __launch_bounds__(RT) k_attn(const float* __restrict__ q_norm, const float* __restrict__ v_scale,
+                                             const int8_t* __restrict__ kq, const float* __restrict__ sk,
+                                             const int16_t* __restrict__ vq, const float* __restrict__ qg,
+                                             const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+                                             int half, float eps, int pos0, int n_h, int n_kv, int hd, float* __restrict__ o) {
+    extern __shared__ float lds[];
+    __shared__ float red[RT / 64];
+    __shared__ int pqs[KC];
+    __shared__ long long dens[RT / 64];
+    float* x = lds;
+    float* s = x + hd;
+    float* t = s + p2(hd);
+    int8_t* qq = reinterpret_cast<int8_t*>(t + p2(hd) / 2 + 1);
+    const int tok = blockIdx.x / n_h, h = blockIdx.x - tok * n_h, pos = pos0 + tok;
+    const int kvh = h / (n_h / n_kv);
+    const float* qr = qg + ((size_t)tok * n_h + h) * 2 * hd;
+    for (int i = threadIdx.x; i < hd; i += RT) x[i] = qr[i];
+    __syncthreads();
+    block_rmsnorm(x, hd, q_norm, eps, s, t);
+    block_rope(x, rope_cos + (size_t)pos * half, rope_sin + (size_t)pos * half, half);
+    const float qscale = 1.0f / __builtin_sqrtf((float)hd);
+    for (int i = threadIdx.x; i < hd; i += RT) x[i] = x[i] * qscale;
+    __syncthreads();
+    const float sq = block_quant_i8(x, hd, qq, red);
+    __syncthreads();
+    const int nkeys = pos + 1, hw = hd / 4;
+    const int* qw = reinterpret_cast<const int*>(qq);
+    auto score = [&](int j) __attribute__((always_inline)) {
+        const int* kw = reinterpret_cast<const int*>(kq + ((size_t)j * n_kv + kvh) * hd);
+        int dot = 0;
+        for (int w = 0; w < hw; w++) dot = __builtin_amdgcn_sdot4(qw[w], kw[w], dot, false);
+        return ((float)dot * sq) * sk[(size_t)j * n_kv + kvh];
+    };
+    // pass 1: the max
+    float mx = -__builtin_inff();
+    for (int j = threadIdx.x; j < nkeys; j += RT) mx = fmax_spec(mx, score(j));
+    mx = wave_fmax(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = -__builtin_inff();
+    for (int w = 0; w < RT / 64; w++) mx = fmax_spec(mx, red[w]);
+    // pass 2: fixed-point weights chunk by chunk; thread i < hd accumulates num_i (dims i, i + RT, ...)
+    constexpr int MAXD = 4;                        // hd <= 1024
+    long long num[MAXD] = {0, 0, 0, 0};
+    long long den = 0;
+    for (int c0 = 0; c0 < nkeys; c0 += KC) {
+        const int nc = min(KC, nkeys - c0);
+        __syncthreads();                           // the previous chunk's weights are consumed
+        for (int jj = threadIdx.x; jj < nc; jj += RT) {
+            const int pq = (int)rint_(exp_f(score(c0 + jj) - mx) * 16777216.0f);   // 0 .. 2^24
+            pqs[jj] = pq;
+            den += pq;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int d = 0; d < MAXD; d++) {
+            const int i = threadIdx.x + d * RT;
+            if (i < hd) {
+                const int16_t* vc = vq + ((size_t)c0 * n_kv + kvh) * hd + i;
+                long long a = num[d];
+                for (int jj = 0; jj < nc; jj++) a += (long long)pqs[jj] * (long long)vc[(size_t)jj * n_kv * hd];
+                num[d] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off, 64);
+    if ((threadIdx.x & 63) == 0) dens[threadIdx.x >> 6] = den;
+    __syncthreads();
+    den = 0;
+    for (int w = 0; w < RT / 64; w++) den += dens[w];
+    const float fden = i64_to_f(den), vs = v_scale[kvh];
+    const float* gate = qr + hd;
+    float* oh = o + ((size_t)tok * n_h + h) * hd;
+#pragma unroll
+    for (int d = 0; d < MAXD; d++) {
+        const int i = threadIdx.x + d * RT;
+        if (i < hd) oh[i] = ((i64_to_f(num[d]) / fden) * vs) * sigmoid_f(gate[i]);
+    }
+}
+
+// ------------------------------------------------------------------ Gated DeltaNet (cpu.rs:287-383)
+// conv + silu of every token's channels at once: window (t - 3, t - 2, t - 1, t), rows before the call from
+// conv_state[3][cd] (oldest first).  grid (M, ceil(cd / RT)).
+__global__ void __launch_bounds__(RT) k_gdn_conv(const float* __restrict__ conv_w, const float* __restrict__ conv_state,
+                                                 const float* __restrict__ qkv, int cd, float* __restrict__ y) {
+    const int tok = blockIdx.x, c = blockIdx.y * RT + threadIdx.x;
+    if (c >= cd) return;
+    float win[4];
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        const int u = tok - 3 + r;
+        win[r] = u >= 0 ? qkv[(size_t)u * cd + c] : conv_state[(size_t)(3 + u) * cd + c];
+    }
+    win[3] = qkv[(size_t)tok * cd + c];
+    const float* w = conv_w + (size_t)c * 4;
+    float acc = (w[0] * win[0]) + (w[1] * win[1]);   // spec/layers.rs:132-138
+    acc = acc + (w[2] * win[2]);
+    acc = acc + (w[3] * win[3]);
+    y[(size_t)tok * cd + c] = silu_f(acc);
+}
+
+// the conv window after the call: the last three inputs (rows of the old window when M < 3); one thread per
+// channel reads its three old rows before writing
+__global__ void __launch_bounds__(RT) k_gdn_conv_state(float* __restrict__ conv_state, const float* __restrict__ qkv,
+                                                       int M, int cd) {
+    const int c = blockIdx.x * RT + threadIdx.x;
+    if (c >= cd) return;
+    const float o0 = conv_state[c], o1 = conv_state[(size_t)cd + c], o2 = conv_state[2 * (size_t)cd + c];
+    float nw[3];
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        const int u = M - 3 + r;                   // input index of new row r; old row u + 3 when u < 0
+        nw[r] = u >= 0 ? qkv[(size_t)u * cd + c] : (u == -3 ? o0 : u == -2 ? o1 : o2);
+    }
+#pragma unroll
+    for (int r = 0; r < 3; r++) conv_state[(size_t)r * cd + c] = nw[r];
+}
+
+// one workgroup per (token, k head): q = l2norm(conv q) * QSCALE, k = l2norm(conv k) (spec/prim.rs:183-190), and
+// for the head's rep v heads beta = sigmoid(b), decay = exp(-(A softplus(a + dt_bias))) (spec/layers.rs:140-143)
+__global__ void __launch_bounds__(RT) k_gdn_prep(const float* __restrict__ y, const float* __restrict__ A,
+                                                 const float* __restrict__ dt_bias, const float* __restrict__ a,
+                                                 const float* __restrict__ b, float eps, int n_k, int n_v, int dk, int cd,
+                                                 float* __restrict__ qb, float* __restrict__ kb, float* __restrict__ bd) {
+    extern __shared__ float lds[];
+    float* x = lds;
+    float* s = x + dk;
+    float* t = s + p2(dk);
+    const int tok = blockIdx.x / n_k, kh = blockIdx.x - tok * n_k, rep = n_v / n_k;
+    const float qscale = __uint_as_float(0x3DB504F3u);            // spec/layers.rs:146
+    for (int part = 0; part < 2; part++) {
+        const float* src = y + (size_t)tok * cd + (size_t)part * n_k * dk + (size_t)kh * dk;
+        for (int i = threadIdx.x; i < dk; i += RT) x[i] = src[i];
+        __syncthreads();
+        const float inv = 1.0f / __builtin_sqrtf(block_treesum<true>(x, dk, s, t) + eps);
+        float* dst = (part == 0 ? qb : kb) + ((size_t)tok * n_k + kh) * dk;
+        for (int i = threadIdx.x; i < dk; i += RT) dst[i] = part == 0 ? (x[i] * inv) * qscale : x[i] * inv;
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < rep; i += RT) {
+        const int hv = kh * rep + i;
+        const size_t ti = (size_t)tok * n_v + hv;
+        bd[2 * ti] = sigmoid_f(b[ti]);
+        bd[2 * ti + 1] = exp_f(-(A[hv] * softplus_f(a[ti] + dt_bias[hv])));
+    }
+}
+
+// balanced tree over the RB values of v (adjacent pairs level by level): the aligned subtree of the spec's tree
+template <int RB>
+__device__ __forceinline__ float reg_tree(float* v) {
+#pragma unroll
+    for (int w = RB >> 1; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; i++) v[i] = v[2 * i] + v[2 * i + 1];
+    return v[0];
+}
+
+// The recurrence of one v head over the M tokens in order (spec/layers.rs:90-130).  Column j of S[h] (dk rows)
+// is split over R = 4 adjacent lanes, lane r holding rows RB r .. RB r + RB - 1 (RB = dk / 4; dk a power of two),
+// so a column's treesum is the lane's subtree then two shuffles that add the subtrees in tree order
+// ((T0 + T1) + (T2 + T3); fp32 addition commutes).  Per token the head's k and q come through LDS.
+template <int RB>
+__global__ void __launch_bounds__(1024) k_gdn_rec(float* __restrict__ S, const float* __restrict__ qb,
+                                                  const float* __restrict__ kb, const float* __restrict__ y,
+                                                  const float* __restrict__ bd, int M, int n_k, int n_v, int dv, int cd,
+                                                  float* __restrict__ ob) {
+    constexpr int R = 4, DK = R * RB;
+    __shared__ float ks[DK], qs[DK];
+    const int h = blockIdx.x, kh = h / (n_v / n_k);
+    const int j = threadIdx.x / R, r = threadIdx.x % R;
+    const bool live = j < dv;
+    float col[RB];
+    float* Sh = S + (size_t)h * DK * dv;
+#pragma unroll
+    for (int i = 0; i < RB; i++) col[i] = live ? Sh[(size_t)(r * RB + i) * dv + j] : 0.0f;
+    const size_t vbase = (size_t)2 * n_k * DK + (size_t)h * dv;      // v of head h inside a token's conv outputs
+    for (int tok = 0; tok < M; tok++) {
+        __syncthreads();                                            // the previous token's k, q are consumed
+        for (int i = threadIdx.x; i < DK; i += blockDim.x) {
+            ks[i] = kb[((size_t)tok * n_k + kh) * DK + i];
+            qs[i] = qb[((size_t)tok * n_k + kh) * DK + i];
+        }
+        __syncthreads();
+        const float beta = bd[2 * ((size_t)tok * n_v + h)], decay = bd[2 * ((size_t)tok * n_v + h) + 1];
+        const float vj = live ? y[(size_t)tok * cd + vbase + j] : 0.0f;
+        float p[RB];
+#pragma unroll
+        for (int i = 0; i < RB; i++) col[i] = col[i] * decay;
+#pragma unroll
+        for (int i = 0; i < RB; i++) p[i] = col[i] * ks[r * RB + i];
+        float kv = reg_tree<RB>(p);
+        kv = kv + __shfl_xor(kv, 1, 64);
+        kv = kv + __shfl_xor(kv, 2, 64);
+        const float delta = (vj - kv) * beta;
+#pragma unroll
+        for (int i = 0; i < RB; i++) col[i] = col[i] + (ks[r * RB + i] * delta);
+#pragma unroll
+        for (int i = 0; i < RB; i++) p[i] = col[i] * qs[r * RB + i];
+        float oj = reg_tree<RB>(p);
+        oj = oj + __shfl_xor(oj, 1, 64);
+        oj = oj + __shfl_xor(oj, 2, 64);
+        if (live && r == 0) ob[((size_t)tok * n_v + h) * dv + j] = oj;
+    }
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < RB; i++) Sh[(size_t)(r * RB + i) * dv + j] = col[i];
+    }
+}
+
+// gated norm: on = rmsnorm(o, norm) * silu(z) per (token, v head)
+__global__ void __launch_bounds__(RT) k_gdn_out(const float* __restrict__ ob, const float* __restrict__ norm,
+                                                const float* __restrict__ z, float eps, int dv, float* __restrict__ on) {
+    extern __shared__ float lds[];
+    float* x = lds;
+    float* s = x + dv;
+    float* t = s + p2(dv);
+    const size_t base = (size_t)blockIdx.x * dv;
+    for (int i = threadIdx.x; i < dv; i += RT) x[i] = ob[base + i];
+    __syncthreads();
+    block_rmsnorm(x, dv, norm, eps, s, t);
+    for (int i = threadIdx.x; i < dv; i += RT) on[base + i] = x[i] * silu_f(z[base + i]);
+}
+
+// ------------------------------------------------------------------ argmax (spec/sample.rs:6-14)
+// the first index of the largest value: every thread scans its indices in increasing order with a strict >, the
+// block keeps the larger value and, on equal values, the lower index
+__global__ void __launch_bounds__(1024) k_argmax(const float* __restrict__ logits, int V, int* __restrict__ out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const float* l = logits + (size_t)blockIdx.x * V;
+    float best = -__builtin_inff();
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += blockDim.x)
+        if (idx == 0x7fffffff || l[i] > best) { best = l[i]; idx = i; }
+    auto better = [](float v, int i, float w, int k) { return k != 0x7fffffff && (i == 0x7fffffff || w > v || (w == v && k < i)); };
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float w = __shfl_xor(best, off, 64);
+        const int k = __shfl_xor(idx, off, 64);
+        if (better(best, idx, w, k)) { best = w; idx = k; }
+    }
+    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)      // lane 0 already holds wave 0's pick
+            if (better(best, idx, bv[w], bi[w])) { best = bv[w]; idx = bi[w]; }
+        out[blockIdx.x] = idx == 0x7fffffff ? 0 : idx;
+    }
+}
+
+size_t gdn_scratch_floats(int M, int n_k, int n_v, int dk, int dv) {
+    const size_t cd = 2 * (size_t)n_k * dk + (size_t)n_v * dv;
+    return (size_t)M * cd + 2 * (size_t)M * n_k * dk + 2 * (size_t)M * n_v + (size_t)M * n_v * dv;
+}
+
+} // namespace
+
+extern "C" {
+
+size_t det_attn_scratch_bytes(int M, int n_h, int hd) { (void)M; (void)n_h; (void)hd; return 0; }
+
+void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float* qg, const float* k, const float* v,
+                   const float* rope_cos, const float* rope_sin, int rot, float eps, int M, int pos0, int n_h, int n_kv,
+                   int hd, float* o, void* scratch, hipStream_t st) {
+    (void)scratch;
+    if (M < 1) return;
+    if (hd < 4 || hd > 1024 || hd % 4) DET_FAIL("det_attention: head_dim %d (multiple of 4, at most 1024)", hd);
+    if (n_kv < 1 || n_h < n_kv || n_h % n_kv) DET_FAIL("det_attention: %d heads over %d kv heads", n_h, n_kv);
+    if (rot < 0 || rot > hd || rot % 2) DET_FAIL("det_attention: rot %d for head_dim %d", rot, hd);
+    if (pos0 < 0 || (long long)pos0 + M > kv->capacity) DET_FAIL("det_attention: positions %d..%d exceed the cache of %d", pos0, pos0 + M - 1, kv->capacity);
+    int p = 1;
+    while (p < hd) p <<= 1;
+    const size_t lds = ((size_t)hd + p + p / 2 + 1) * 4 + (size_t)hd;
+    k_attn_kv<<<M * n_kv, RT, lds, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, rope_cos, rope_sin,
+                                         rot / 2, eps, pos0, n_kv, hd);
+    DET_CHECK(hipGetLastError());
+    k_attn<<<M * n_h, RT, lds, st>>>(L->q_norm, L->v_scale, kv->kq, kv->sk, kv->vq, qg, rope_cos, rope_sin, rot / 2, eps,
+                                     pos0, n_h, n_kv, hd, o);
+    DET_CHECK(hipGetLastError());
+}
+
+size_t det_gdn_scratch_bytes(int M, int n_k, int n_v, int dk, int dv) {
+    return gdn_scratch_floats(M < 1 ? 1 : M, n_k, n_v, dk, dv) * sizeof(float);
+}
+
+void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const float* z, const float* a, const float* b,
+             float eps, int M, int n_k, int n_v, int dk, int dv, float* on, void* scratch, hipStream_t st) {
+    if (M < 1) return;
+    if (n_k < 1 || n_v < n_k || n_v % n_k) DET_FAIL("det_gdn: %d v heads over %d k heads", n_v, n_k);
+    if (dk < 4 || dk > 128 || (dk & (dk - 1))) DET_FAIL("det_gdn: dk %d (a power of two, 4 .. 128)", dk);
+    if (dv < 1 || dv > 256) DET_FAIL("det_gdn: dv %d (at most 256)", dv);
+    if (!scratch) DET_FAIL("det_gdn: scratch of det_gdn_scratch_bytes() is required");
+    const int cd = 2 * n_k * dk + n_v * dv;
+    float* y = static_cast<float*>(scratch);
+    float* qb = y + (size_t)M * cd;
+    float* kb = qb + (size_t)M * n_k * dk;
+    float* bd = kb + (size_t)M * n_k * dk;
+    float* ob = bd + 2 * (size_t)M * n_v;
+    k_gdn_conv<<<dim3(M, (cd + RT - 1) / RT), RT, 0, st>>>(L->conv, S->conv_state, qkv, cd, y);
+    DET_CHECK(hipGetLastError());
+    k_gdn_conv_state<<<(cd + RT - 1) / RT, RT, 0, st>>>(S->conv_state, qkv, M, cd);
+    DET_CHECK(hipGetLastError());
+    int p = 1;
+    while (p < dk) p <<= 1;
+    k_gdn_prep<<<M * n_k, RT, ((size_t)dk + p + p / 2) * 4, st>>>(y, L->A, L->dt_bias, a, b, eps, n_k, n_v, dk, cd, qb, kb, bd);
+    DET_CHECK(hipGetLastError());
+    const int threads = ((dv * 4 + 63) / 64) * 64;
+    switch (dk / 4) {
+    case 1: k_gdn_rec<1><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 2: k_gdn_rec<2><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 4: k_gdn_rec<4><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 8: k_gdn_rec<8><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 16: k_gdn_rec<16><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    default: k_gdn_rec<32><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    }
+    DET_CHECK(hipGetLastError());
+    int pv = 1;
+    while (pv < dv) pv <<= 1;
+    k_gdn_out<<<M * n_v, RT, ((size_t)dv + pv + pv / 2) * 4, st>>>(ob, L->norm, z, eps, dv, on);
+    DET_CHECK(hipGetLastError());
+}
+
+void det_argmax(const float* logits, int M, int V, int* out, hipStream_t st) {
+    if (M < 1) return;
+    if (V < 1) DET_FAIL("det_argmax: V=%d", V);
+    k_argmax<<<M, 1024, 0, st>>>(logits, V, out);
+    DET_CHECK(hipGetLastError());
+}
+
+} // extern "C"

@@ -23,6 +23,29 @@ class QLinear(ctypes.Structure):
                 ('N', ctypes.c_int), ('K', ctypes.c_int), ('bits', ctypes.c_int)]
 
 
+class AttnLayer(ctypes.Structure):
+    """det_attn_layer (det_hip.h; det_cuda.h:60-65)."""
+    _fields_ = [('q_norm', ctypes.c_void_p), ('k_norm', ctypes.c_void_p), ('v_scale', ctypes.c_void_p),
+                ('v_inv_scale', ctypes.c_void_p)]
+
+
+class KvCache(ctypes.Structure):
+    """det_kv_cache (det_hip.h; det_cuda.h:66-67)."""
+    _fields_ = [('kq', ctypes.c_void_p), ('sk', ctypes.c_void_p), ('vq', ctypes.c_void_p), ('capacity', ctypes.c_int),
+                ('vlo', ctypes.c_void_p), ('vhi', ctypes.c_void_p)]
+
+
+class GdnLayer(ctypes.Structure):
+    """det_gdn_layer (det_hip.h; det_cuda.h:85-90)."""
+    _fields_ = [('conv', ctypes.c_void_p), ('A', ctypes.c_void_p), ('dt_bias', ctypes.c_void_p),
+                ('norm', ctypes.c_void_p)]
+
+
+class GdnState(ctypes.Structure):
+    """det_gdn_state (det_hip.h; det_cuda.h:91)."""
+    _fields_ = [('conv_state', ctypes.c_void_p), ('S', ctypes.c_void_p)]
+
+
 def header_symbols():
     """Function names declared in include/det_hip.h."""
     text = open(HEADER).read()
@@ -53,6 +76,12 @@ def lib():
         'det_gemm_ex': (None, [ctypes.POINTER(QLinear), P, P, P, i, P, i, i, P, P, P]),
         'det_gemm_scratch_bytes': (sz, [i, i]), 'det_gemm_set_scratch': (None, [P, sz]),
         'det_test_prim': (None, [i, P, i, i, P, P]),
+        'det_attention': (None, [ctypes.POINTER(AttnLayer), ctypes.POINTER(KvCache), P, P, P, P, P, i, f, i, i, i, i,
+                                 i, P, P, P]),
+        'det_attn_scratch_bytes': (sz, [i, i, i]),
+        'det_gdn': (None, [ctypes.POINTER(GdnLayer), ctypes.POINTER(GdnState), P, P, P, P, f, i, i, i, i, i, P, P, P]),
+        'det_gdn_scratch_bytes': (sz, [i, i, i, i, i]),
+        'det_argmax': (None, [P, i, i, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -179,3 +208,24 @@ def test_prim(op, x, M, n):
     out = Buf(M if op == 11 else M * n, np.float32)
     lib().det_test_prim(op, xb.ptr, M, n, out.ptr, None)
     return out.download()
+
+
+def attention(layer, kv, qg, k, v, rope_cos, rope_sin, rot, eps, M, pos0, n_h, n_kv, hd, o):
+    """Backend::attention (backend.rs; cpu.rs:212-285) over det_attention.  layer: AttnLayer, kv: KvCache."""
+    lib().det_attention(ctypes.byref(layer), ctypes.byref(kv), qg.ptr, k.ptr, v.ptr, rope_cos.ptr, rope_sin.ptr, rot,
+                        eps, M, pos0, n_h, n_kv, hd, o.ptr, None, None)
+
+
+def gdn(layer, state, qkv, z, a, b, eps, M, n_k, n_v, dk, dv, on, scratch):
+    """Backend::gdn (backend.rs; cpu.rs:287-383) over det_gdn.  scratch: a Buf of det_gdn_scratch_bytes()."""
+    lib().det_gdn(ctypes.byref(layer), ctypes.byref(state), qkv.ptr, z.ptr, a.ptr, b.ptr, eps, M, n_k, n_v, dk, dv,
+                  on.ptr, scratch.ptr, None)
+
+
+def gdn_scratch_bytes(M, n_k, n_v, dk, dv):
+    return lib().det_gdn_scratch_bytes(M, n_k, n_v, dk, dv)
+
+
+def argmax(logits, M, V, out):
+    """Backend::argmax (backend.rs; spec/sample.rs:6-14) over det_argmax: out[m] = first index of the max."""
+    lib().det_argmax(logits.ptr, M, V, out.ptr, None)

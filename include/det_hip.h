@@ -79,6 +79,45 @@ void det_gemm_ex(const det_qlinear* L, const int8_t* xq, const float* sx, const 
 size_t det_gemm_scratch_bytes(int M, int K);
 void det_gemm_set_scratch(void* p, size_t bytes);
 
+// ---- attention (replaces kernels/cuda/attn.cu; det_cuda.h:60-76, cpu.rs:212-285)
+typedef struct {
+    const float* q_norm;      // [hd]
+    const float* k_norm;      // [hd]
+    const float* v_scale;     // [n_kv]
+    const float* v_inv_scale; // [n_kv]
+} det_attn_layer;
+// vlo / vhi are kept for the reference's signature (its Metal runtime's V planes); unused here.
+typedef struct { int8_t* kq; float* sk; int16_t* vq; int capacity; int8_t* vlo; int8_t* vhi; } det_kv_cache;
+// M new tokens at positions pos0 .. pos0 + M - 1: qg[M][n_h][2 hd] (per head q | gate), k, v [M][n_kv][hd], rope
+// tables [pos][rot / 2].  Writes the cache rows (kq[pos][n_kv][hd] int8, sk[pos][n_kv], vq[pos][n_kv][hd] int16),
+// attends every new token to the positions <= its own, gates by sigmoid(gate) and writes o[M][n_h][hd].
+// hd a multiple of 4 up to 1024, n_h a multiple of n_kv, rot even and <= hd, pos0 + M <= capacity, else abort().
+// This backend needs no scratch (det_attn_scratch_bytes returns 0; scratch may be NULL).
+void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float* qg, const float* k, const float* v,
+                   const float* rope_cos, const float* rope_sin, int rot, float eps,
+                   int M, int pos0, int n_h, int n_kv, int hd, float* o, void* scratch, hipStream_t st);
+size_t det_attn_scratch_bytes(int M, int n_h, int hd);
+
+// ---- Gated DeltaNet (replaces kernels/cuda/gdn.cu; det_cuda.h:85-98, cpu.rs:287-383)
+typedef struct {
+    const float* conv;     // [conv_dim][4]
+    const float* A;        // [n_v]  (the negated ssm_a of the file)
+    const float* dt_bias;  // [n_v]
+    const float* norm;     // [dv]
+} det_gdn_layer;
+typedef struct { float* conv_state; /* [3][conv_dim] oldest first */ float* S; /* [n_v][dk][dv] */ } det_gdn_state;
+// qkv[M][conv_dim] (conv_dim = 2 n_k dk + n_v dv), z[M][n_v][dv], a, b [M][n_v]: conv + silu, l2norm of q (times
+// QSCALE) and k, the recurrence over the M tokens in order (updating S and the conv window), gated rmsnorm with
+// silu(z); writes on[M][n_v][dv].  dk a power of two in 4 .. 128, dv <= 256, n_v a multiple of n_k, scratch of at
+// least det_gdn_scratch_bytes(M, ...) bytes, else abort().
+void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const float* z, const float* a, const float* b,
+             float eps, int M, int n_k, int n_v, int dk, int dv, float* on, void* scratch, hipStream_t st);
+size_t det_gdn_scratch_bytes(int M, int n_k, int n_v, int dk, int dv);
+
+// ---- argmax (replaces det_argmax of runtime.cu; det_cuda.h:43, spec/sample.rs:6-14): out[m] = the lowest index of
+// the largest of logits[m][0 .. V)
+void det_argmax(const float* logits, int M, int V, int* out, hipStream_t st);
+
 // ---- test hooks (replaces det_test_prim of runtime.cu; det_cuda.h:114-118): elementwise fp32 primitives on arrays,
 // for bit-exactness tests vs the spec.
 // op: 0 exp_f, 1 log_f, 2 softplus_f, 3 sigmoid_f, 4 silu_f, 5 i64->f32 of (long long) bits of x pairs (x[2i],x[2i+1]),
