@@ -186,3 +186,56 @@ def convert_ref(model, bits='6,output=8,ssm_alpha=8,ssm_beta=8', rope_positions=
         blobs.append(data + bytes(-len(data) % 32))
         off += len(blobs[-1])
     return header(out_kv, infos, 32) + b''.join(blobs)
+
+
+def read_gguf(data):
+    """A GGUF file's bytes -> ({key: (type, value)}, {name: (dims, type, data bytes)}) (gguf.rs:208-300 restated
+    for the test side: the oracle model reads the converter restatement's output through this, not the library)."""
+    pos = 0
+
+    def take(n):
+        nonlocal pos
+        b = data[pos:pos + n]
+        pos += n
+        return b
+
+    def u32():
+        return struct.unpack('<I', take(4))[0]
+
+    def u64():
+        return struct.unpack('<Q', take(8))[0]
+
+    def string():
+        return take(u64()).decode()
+
+    def value(ty):
+        if ty == STR:
+            return string()
+        if ty == ARRAY:
+            et, n = u32(), u64()
+            return (et, [value(et) for _ in range(n)])
+        fmt = _FMT[ty]
+        return struct.unpack(fmt, take(struct.calcsize(fmt)))[0]
+
+    assert take(4) == b'GGUF'
+    u32()
+    n_t, n_kv = u64(), u64()
+    kv = {}
+    for _ in range(n_kv):
+        k = string()
+        ty = u32()
+        kv[k] = (ty, value(ty))
+    infos = []
+    for _ in range(n_t):
+        name = string()
+        dims = [u64() for _ in range(u32())]
+        infos.append((name, dims, u32(), u64()))
+    align = kv.get('general.alignment', (U32, 32))[1]
+    start = (pos + align - 1) // align * align
+    tensors = {}
+    for name, dims, ty, off in infos:
+        k = dims[0]
+        rb = 4 * k if ty == T_F32 else 2 * k if ty in (T_F16, T_BF16) else oracle.row_bytes({v: b for b, v in DET.items()}[ty], k)
+        rows = int(np.prod(dims[1:])) if len(dims) > 1 else 1
+        tensors[name] = (dims, ty, data[start + off:start + off + rb * rows])
+    return kv, tensors
