@@ -176,6 +176,117 @@ def cpu_baseline(target_s=10.0):
                       f'the whole W6 K=2560 N=9728 M=512 GEMM {reps} times in {dt:.1f} s'}
 
 
+# ---------------------------------------------------------------- end to end
+QWEN35_4B = dict(hidden=2560, layers=32, interval=4, ff=9728, heads=16, kv=4, hd=256, rot=64, nk=16, nv=32, dk=128,
+                 dv=128, vocab=248320, ctx=640)
+
+
+def write_qwen35_bf16(path, cfg, seed):
+    """A random-init qwen35 float GGUF of the given architecture (weights seeded N(0, 0.02), norms 1 + N(0, 0.02),
+    ssm_a negative), BF16 matrices and F32 vectors, streamed to disk tensor by tensor."""
+    import struct
+    H, FF, V = cfg['hidden'], cfg['ff'], cfg['vocab']
+    cd = 2 * cfg['nk'] * cfg['dk'] + cfg['nv'] * cfg['dv']
+    qd, kvd, od = 2 * cfg['heads'] * cfg['hd'], cfg['kv'] * cfg['hd'], cfg['heads'] * cfg['hd']
+    ts = [('token_embd.weight', [H, V], 'w'), ('output_norm.weight', [H], 'n'), ('output.weight', [H, V], 'w')]
+    for i in range(cfg['layers']):
+        b = f'blk.{i}.'
+        ts += [(b + 'attn_norm.weight', [H], 'n'), (b + 'post_attention_norm.weight', [H], 'n'),
+               (b + 'ffn_gate.weight', [H, FF], 'w'), (b + 'ffn_up.weight', [H, FF], 'w'),
+               (b + 'ffn_down.weight', [FF, H], 'w')]
+        if (i + 1) % cfg['interval'] == 0:
+            ts += [(b + 'attn_q.weight', [H, qd], 'w'), (b + 'attn_k.weight', [H, kvd], 'w'),
+                   (b + 'attn_v.weight', [H, kvd], 'w'), (b + 'attn_output.weight', [od, H], 'w'),
+                   (b + 'attn_q_norm.weight', [cfg['hd']], 'n'), (b + 'attn_k_norm.weight', [cfg['hd']], 'n')]
+        else:
+            ts += [(b + 'attn_qkv.weight', [H, cd], 'w'), (b + 'attn_gate.weight', [H, cfg['nv'] * cfg['dv']], 'w'),
+                   (b + 'ssm_alpha.weight', [H, cfg['nv']], 'w'), (b + 'ssm_beta.weight', [H, cfg['nv']], 'w'),
+                   (b + 'ssm_out.weight', [cfg['nv'] * cfg['dv'], H], 'w'), (b + 'ssm_conv1d.weight', [4, cd], 'c'),
+                   (b + 'ssm_a', [cfg['nv']], 'a'), (b + 'ssm_dt.bias', [cfg['nv']], 'c'),
+                   (b + 'ssm_norm.weight', [cfg['dv']], 'n')]
+    U32, F32, STR = 4, 6, 8
+    kv = [('general.architecture', STR, 'qwen35'), ('qwen35.block_count', U32, cfg['layers']),
+          ('qwen35.full_attention_interval', U32, cfg['interval']), ('qwen35.embedding_length', U32, H),
+          ('qwen35.feed_forward_length', U32, FF), ('qwen35.attention.head_count', U32, cfg['heads']),
+          ('qwen35.attention.head_count_kv', U32, cfg['kv']), ('qwen35.attention.key_length', U32, cfg['hd']),
+          ('qwen35.attention.layer_norm_rms_epsilon', F32, 1e-6), ('qwen35.rope.dimension_count', U32, cfg['rot']),
+          ('qwen35.rope.freq_base', F32, 10000000.0), ('qwen35.context_length', U32, cfg['ctx']),
+          ('qwen35.ssm.state_size', U32, cfg['dk']), ('qwen35.ssm.time_step_rank', U32, cfg['nv']),
+          ('qwen35.ssm.group_count', U32, cfg['nk']), ('qwen35.ssm.inner_size', U32, cfg['nv'] * cfg['dv']),
+          ('qwen35.ssm.conv_kernel', U32, 4)]
+    sizes = [int(np.prod(d)) * (2 if k == 'w' else 4) for _, d, k in ts]
+    head = bytearray(b'GGUF') + struct.pack('<IQQ', 3, len(ts), len(kv))
+    for key, ty, v in kv:
+        head += struct.pack('<Q', len(key)) + key.encode() + struct.pack('<I', ty)
+        head += (struct.pack('<Q', len(v)) + v.encode()) if ty == STR else struct.pack('<f' if ty == F32 else '<I', v)
+    off = 0
+    for (name, dims, kind), nb in zip(ts, sizes):
+        head += struct.pack('<Q', len(name)) + name.encode() + struct.pack('<I', len(dims))
+        head += b''.join(struct.pack('<Q', d) for d in dims) + struct.pack('<IQ', 30 if kind == 'w' else 0, off)
+        off += nb + (-nb % 32)
+    head += bytes(-len(head) % 32)
+    with open(path, 'wb') as f:
+        f.write(head)
+        for idx, ((name, dims, kind), nb) in enumerate(zip(ts, sizes)):
+            rng = np.random.default_rng([seed, idx])
+            n = int(np.prod(dims))
+            a = rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)
+            if kind == 'n':
+                a = a + np.float32(1)
+            elif kind == 'a':
+                a = -np.abs(a) - np.float32(1)
+            data = (a.view(np.uint32) >> 16).astype(np.uint16).tobytes() if kind == 'w' else a.tobytes()
+            f.write(data + bytes(-len(data) % 32))
+            if idx % 40 == 0:
+                print(f'e2e: writing tensor {idx} of {len(ts)}', file=sys.stderr, flush=True)
+
+
+def e2e(args):
+    """the 4B-architecture model converted by det convert, prefill 512 ids, greedy decode 128."""
+    import tempfile
+    from det_amd import gguf, model
+    cfg = dict(QWEN35_4B)
+    L = ffi.lib()
+    assert L.det_init() == 0
+    tmp = tempfile.mkdtemp(prefix='det_e2e_')
+    src, dst = os.path.join(tmp, 'q35-4b-BF16.gguf'), os.path.join(tmp, 'q35-4b-det-w6.gguf')
+    t0 = time.time()
+    write_qwen35_bf16(src, cfg, seed=5)
+    t1 = time.time()
+    print(f'e2e: bf16 source written ({os.path.getsize(src) / 1e9:.2f} GB, {t1 - t0:.1f} s)', file=sys.stderr, flush=True)
+    gguf.convert(src, dst, None, cfg['ctx'])
+    os.remove(src)
+    t2 = time.time()
+    print(f'e2e: det convert done ({os.path.getsize(dst) / 1e9:.2f} GB, {t2 - t1:.1f} s)', file=sys.stderr, flush=True)
+    m = model.Model(dst, cfg['ctx'], 512)
+    t3 = time.time()
+    print(f'e2e: model loaded ({t3 - t2:.1f} s)', file=sys.stderr, flush=True)
+    prompt = np.random.default_rng(11).integers(0, cfg['vocab'], 512).tolist()
+    m.prefill(prompt)                              # warm-up pass (code objects, caches), then the measured one
+    m.generate([], 4)
+    m.reset()
+    L.det_sync()
+    a = time.perf_counter()
+    m.prefill(prompt)
+    L.det_sync()
+    b = time.perf_counter()
+    toks = m.generate([], args.decode)
+    L.det_sync()
+    c = time.perf_counter()
+    os.remove(dst)
+    os.rmdir(tmp)
+    out = {'metric': 'end-to-end qwen35 4B-architecture: prefill and greedy decode tokens/s, 1 MI355X',
+           'prefill_tok_s': round(512 / (b - a), 1), 'decode_tok_s': round(len(toks) / (c - b), 2),
+           'prefill_ms': round((b - a) * 1e3, 2), 'decode_ms_per_token': round((c - b) * 1e3 / max(len(toks), 1), 3),
+           'tokens': toks[:8], 'n_decoded': len(toks), 'unit': 'tokens/s', 'higher_is_better': True,
+           'data': 'synthetic (random-init weights, seed 5; prompt of 512 uniform ids, seed 11)',
+           'config': {'workload': 'BASELINE configs[4]', **cfg,
+                      'bits': '6,output=8,ssm_alpha=8,ssm_beta=8 (det convert default, --no-calibrate)',
+                      'max_batch': 512},
+           'setup_s': {'write_bf16': round(t1 - t0, 1), 'convert': round(t2 - t1, 1), 'load': round(t3 - t2, 1)}}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -185,7 +296,13 @@ def main():
     ap.add_argument('--only-main', action='store_true')
     ap.add_argument('--copy-calibration', action='store_true',
                     help='only run a plain device-to-device copy of 1 GiB, 10 times (scales FETCH_SIZE/WRITE_SIZE)')
+    ap.add_argument('--e2e', action='store_true',
+                    help='BASELINE configs[4] instead: the 4B-architecture model end to end (prefill / decode tokens/s)')
+    ap.add_argument('--decode', type=int, default=128, help='tokens decoded by --e2e')
     args = ap.parse_args()
+    if args.e2e:
+        e2e(args)
+        return
     if args.copy_calibration:
         L = ffi.lib()
         a, b = ffi.Buf(1 << 30, np.uint8), ffi.Buf(1 << 30, np.uint8)
