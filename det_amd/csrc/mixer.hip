@@ -275,50 +275,69 @@ __device__ __forceinline__ float reg_tree(float* v) {
 }
 
 // The recurrence of one v head over the M tokens in order (spec/layers.rs:90-130).  Column j of S[h] (dk rows)
-// is split over R = 4 adjacent lanes, lane r holding rows RB r .. RB r + RB - 1 (RB = dk / 4; dk a power of two),
-// so a column's treesum is the lane's subtree then two shuffles that add the subtrees in tree order
-// ((T0 + T1) + (T2 + T3); fp32 addition commutes).  Per token the head's k and q come through LDS.
-template <int RB>
+// is split over R adjacent lanes, lane r holding rows RB r .. RB r + RB - 1 (dk = R RB, a power of two), so a
+// column's treesum is the lane's subtree, then log2(R) shuffle levels that add the aligned subtrees in tree order
+// (pairs, then pairs of pairs; fp32 addition commutes).  The columns evolve independently, so a head's dv columns
+// are spread over blocks of CW columns (grid y), one workgroup each.  Every TC tokens a workgroup stages their k, q
+// (of the head's k head), its columns' v, beta and decay in LDS with one burst of loads, so the token loop itself
+// reads only LDS.
+template <int RB, int R>
 __global__ void __launch_bounds__(1024) k_gdn_rec(float* __restrict__ S, const float* __restrict__ qb,
                                                   const float* __restrict__ kb, const float* __restrict__ y,
                                                   const float* __restrict__ bd, int M, int n_k, int n_v, int dv, int cd,
-                                                  float* __restrict__ ob) {
-    constexpr int R = 4, DK = R * RB;
-    __shared__ float ks[DK], qs[DK];
-    const int h = blockIdx.x, kh = h / (n_v / n_k);
-    const int j = threadIdx.x / R, r = threadIdx.x % R;
-    const bool live = j < dv;
+                                                  int CW, float* __restrict__ ob) {
+    constexpr int DK = R * RB, TC = 32;
+    extern __shared__ float sm[];
+    float* ks = sm;                       // [TC][DK]
+    float* qs = ks + TC * DK;             // [TC][DK]
+    float* bt = qs + TC * DK;             // [TC][2] beta, decay
+    float* vs = bt + 2 * TC;              // [TC][CW] v of this block's columns
+    const int h = blockIdx.x, kh = h / (n_v / n_k), j0 = blockIdx.y * CW;
+    const int jl = threadIdx.x / R, r = threadIdx.x % R, j = j0 + jl;
+    const bool live = jl < CW && j < dv;
     float col[RB];
     float* Sh = S + (size_t)h * DK * dv;
 #pragma unroll
     for (int i = 0; i < RB; i++) col[i] = live ? Sh[(size_t)(r * RB + i) * dv + j] : 0.0f;
     const size_t vbase = (size_t)2 * n_k * DK + (size_t)h * dv;      // v of head h inside a token's conv outputs
-    for (int tok = 0; tok < M; tok++) {
-        __syncthreads();                                            // the previous token's k, q are consumed
-        for (int i = threadIdx.x; i < DK; i += blockDim.x) {
-            ks[i] = kb[((size_t)tok * n_k + kh) * DK + i];
-            qs[i] = qb[((size_t)tok * n_k + kh) * DK + i];
+    for (int c0 = 0; c0 < M; c0 += TC) {
+        const int nt = min(TC, M - c0);
+        __syncthreads();                                            // the previous chunk is consumed
+        for (int e = threadIdx.x; e < nt * DK; e += blockDim.x) {
+            const int tt = e / DK, i = e - tt * DK;
+            const size_t src = ((size_t)(c0 + tt) * n_k + kh) * DK + i;
+            ks[e] = kb[src];
+            qs[e] = qb[src];
         }
+        for (int e = threadIdx.x; e < nt * CW; e += blockDim.x) {
+            const int tt = e / CW, jj = e - tt * CW;
+            vs[e] = j0 + jj < dv ? y[(size_t)(c0 + tt) * cd + vbase + j0 + jj] : 0.0f;
+        }
+        for (int e = threadIdx.x; e < 2 * nt; e += blockDim.x) bt[e] = bd[2 * ((size_t)(c0 + e / 2) * n_v + h) + (e & 1)];
         __syncthreads();
-        const float beta = bd[2 * ((size_t)tok * n_v + h)], decay = bd[2 * ((size_t)tok * n_v + h) + 1];
-        const float vj = live ? y[(size_t)tok * cd + vbase + j] : 0.0f;
-        float p[RB];
+        for (int tt = 0; tt < nt; tt++) {
+            const float* kt = ks + tt * DK + r * RB;
+            const float* qt = qs + tt * DK + r * RB;
+            const float beta = bt[2 * tt], decay = bt[2 * tt + 1];
+            const float vj = live ? vs[tt * CW + jl] : 0.0f;
+            float p[RB];
 #pragma unroll
-        for (int i = 0; i < RB; i++) col[i] = col[i] * decay;
+            for (int i = 0; i < RB; i++) col[i] = col[i] * decay;
 #pragma unroll
-        for (int i = 0; i < RB; i++) p[i] = col[i] * ks[r * RB + i];
-        float kv = reg_tree<RB>(p);
-        kv = kv + __shfl_xor(kv, 1, 64);
-        kv = kv + __shfl_xor(kv, 2, 64);
-        const float delta = (vj - kv) * beta;
+            for (int i = 0; i < RB; i++) p[i] = col[i] * kt[i];
+            float kv = reg_tree<RB>(p);
 #pragma unroll
-        for (int i = 0; i < RB; i++) col[i] = col[i] + (ks[r * RB + i] * delta);
+            for (int o = 1; o < R; o <<= 1) kv = kv + __shfl_xor(kv, o, 64);
+            const float delta = (vj - kv) * beta;
 #pragma unroll
-        for (int i = 0; i < RB; i++) p[i] = col[i] * qs[r * RB + i];
-        float oj = reg_tree<RB>(p);
-        oj = oj + __shfl_xor(oj, 1, 64);
-        oj = oj + __shfl_xor(oj, 2, 64);
-        if (live && r == 0) ob[((size_t)tok * n_v + h) * dv + j] = oj;
+            for (int i = 0; i < RB; i++) col[i] = col[i] + (kt[i] * delta);
+#pragma unroll
+            for (int i = 0; i < RB; i++) p[i] = col[i] * qt[i];
+            float oj = reg_tree<RB>(p);
+#pragma unroll
+            for (int o = 1; o < R; o <<= 1) oj = oj + __shfl_xor(oj, o, 64);
+            if (live && r == 0) ob[((size_t)(c0 + tt) * n_v + h) * dv + j] = oj;
+        }
     }
     if (live) {
 #pragma unroll
@@ -423,14 +442,21 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
     while (p < dk) p <<= 1;
     k_gdn_prep<<<M * n_k, RT, ((size_t)dk + p + p / 2) * 4, st>>>(y, L->A, L->dt_bias, a, b, eps, n_k, n_v, dk, cd, qb, kb, bd);
     DET_CHECK(hipGetLastError());
-    const int threads = ((dv * 4 + 63) / 64) * 64;
-    switch (dk / 4) {
-    case 1: k_gdn_rec<1><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 2: k_gdn_rec<2><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 4: k_gdn_rec<4><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 8: k_gdn_rec<8><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 16: k_gdn_rec<16><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    default: k_gdn_rec<32><<<n_v, threads, 0, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    // lanes per column: 8 (4 when dk < 8); blocks of CW = 16 columns, one workgroup each (grid y)
+    const int R = dk >= 8 ? 8 : 4, CW = dv < 16 ? dv : 16, CB = (dv + CW - 1) / CW;
+    const int threads = ((CW * R + 63) / 64) * 64;
+    const size_t rl = ((size_t)2 * 32 * dk + 2 * 32 + (size_t)32 * CW) * sizeof(float);
+    const dim3 grid(n_v, CB);
+    if (R == 8) {
+        switch (dk / 8) {
+        case 1: k_gdn_rec<1, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
+        case 2: k_gdn_rec<2, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
+        case 4: k_gdn_rec<4, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
+        case 8: k_gdn_rec<8, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
+        default: k_gdn_rec<16, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
+        }
+    } else {
+        k_gdn_rec<1, 4><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob);
     }
     DET_CHECK(hipGetLastError());
     int pv = 1;

@@ -10,8 +10,9 @@ using namespace det;
 
 namespace {
 
-constexpr int QT = 256;            // threads per row
-constexpr int QW = QT / 64;        // waves per row
+// threads per row: 256 when many rows fill the device, 1024 for a few rows (a lone row's workgroup then has 16
+// waves to overlap its latency-bound reductions); the results do not depend on the count
+constexpr int QT_MANY = 256, QT_FEW = 1024, QT_FEW_MAX_ROWS = 64;
 
 enum { MODE_QUANT = 0, MODE_RMSNORM = 1, MODE_SILU_MUL = 2 };
 
@@ -24,10 +25,11 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // dynamic LDS: v[n] fp32 (the row after its producer op), then for MODE_RMSNORM the tree buffers s[p], t[p/2]
-template <int MODE>
+template <int MODE, int QT>
 __global__ void __launch_bounds__(QT) k_quant(const float* __restrict__ a, const float* __restrict__ b, float eps, int n,
                                               float* __restrict__ y, int8_t* __restrict__ xq, float* __restrict__ sx,
                                               uint16_t* __restrict__ mx) {
+    constexpr int QW = QT / 64;        // waves per row
     extern __shared__ float lds[];
     __shared__ float red[QW];
     __shared__ float sg[1024];
@@ -76,8 +78,9 @@ __global__ void __launch_bounds__(QT) k_quant(const float* __restrict__ a, const
             if (lane == 0) sg[g] = am / 127.0f;
         }
         __syncthreads();
-        float smax = 0.0f;
-        for (int g = 0; g < G; g++) smax = fmax_spec(smax, sg[g]);
+        float smax = 0.0f;                       // fmax fold, order-free: one wave reduction per wave
+        for (int g = lane; g < G; g += 64) smax = fmax_spec(smax, sg[g]);
+        smax = wave_max(smax);
         const float s = smax == 0.0f ? 1.0f : smax / 65535.0f;
         for (int g = wv; g < G; g += QW) {
             float m = rint_(sg[g] / s);
@@ -121,10 +124,12 @@ void launch(const float* a, const float* b, float eps, int M, int n, float* y, i
     if (lds > 150 * 1024) DET_FAIL("%s: row of n=%d does not fit in LDS", who, n);
     static bool attr = false;
     if (!attr) {
-        DET_CHECK(hipFuncSetAttribute((const void*)k_quant<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024));
+        DET_CHECK(hipFuncSetAttribute((const void*)k_quant<MODE, QT_MANY>, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024));
+        DET_CHECK(hipFuncSetAttribute((const void*)k_quant<MODE, QT_FEW>, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024));
         attr = true;
     }
-    k_quant<MODE><<<M, QT, lds, st>>>(a, b, eps, n, y, xq, sx, mx);
+    if (M <= QT_FEW_MAX_ROWS) k_quant<MODE, QT_FEW><<<M, QT_FEW, lds, st>>>(a, b, eps, n, y, xq, sx, mx);
+    else k_quant<MODE, QT_MANY><<<M, QT_MANY, lds, st>>>(a, b, eps, n, y, xq, sx, mx);
     DET_CHECK(hipGetLastError());
 }
 
