@@ -7,6 +7,7 @@
 // power of two (ping-pong LDS levels, or an in-register subtree per lane plus lane shuffles that combine the
 // aligned subtrees in tree order); the attention max is an fmax fold (order-free) and its weighted sums are exact
 // int64 integers (order-free).
+#include <algorithm>
 #include "common.h"
 #include "../../include/det_hip.h"
 using namespace det;
@@ -114,21 +115,28 @@ __global__ void __launch_bounds__(RT) k_attn_kv(const float* __restrict__ k_norm
 // One workgroup per (token, head): q -> rmsnorm(q_norm) -> rope -> * 1/sqrt(hd) -> quant_act_i8 (qq, sq); keys
 // 0 .. pos of kv head h / rep: s_j = (f32(dot(qq, kq_j)) * sq) * sk_j, mx = fmax fold, pq_j = rint(exp(s_j - mx)
 // * 2^24) as int64, den = sum pq_j, num_i = sum pq_j vq_j[i] (exact, order-free), o_i = ((f32(num_i) / f32(den)) *
-// v_scale) * sigmoid(gate_i) (spec/layers.rs:24-69).  The scores are computed twice (max pass, weight pass).
-// LDS: x[hd] floats, tree s[p], t[p / 2], qq[hd] bytes; static: the chunk's weights, den partials.
+// v_scale) * sigmoid(gate_i) (spec/layers.rs:24-69).  The max pass keeps the scores in LDS (up to SMAX keys; longer
+// rows recompute them); the weight pass walks the keys in chunks of kc whose value rows are staged in LDS by
+// coalesced loads, so the numerators read LDS only.
+// Dynamic LDS: x[hd], tree s[p], t[p / 2] floats, qq[hd] bytes, scores sc[SMAX], values vl[kc][hd] int16.
+constexpr int SMAX = 2048;
 __global__ void __launch_bounds__(RT) k_attn(const float* __restrict__ q_norm, const float* __restrict__ v_scale,
                                              const int8_t* __restrict__ kq, const float* __restrict__ sk,
                                              const int16_t* __restrict__ vq, const float* __restrict__ qg,
                                              const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
-                                             int half, float eps, int pos0, int n_h, int n_kv, int hd, float* __restrict__ o) {
+                                             int half, float eps, int pos0, int n_h, int n_kv, int hd, int kc,
+                                             float* __restrict__ o) {
     extern __shared__ float lds[];
     __shared__ float red[RT / 64];
-    __shared__ int pqs[KC];
+    __shared__ int pqs[256];
     __shared__ long long dens[RT / 64];
+    const int p = p2(hd);
     float* x = lds;
     float* s = x + hd;
-    float* t = s + p2(hd);
-    int8_t* qq = reinterpret_cast<int8_t*>(t + p2(hd) / 2 + 1);
+    float* t = s + p;
+    int8_t* qq = reinterpret_cast<int8_t*>(t + p / 2 + 4);
+    float* sc = reinterpret_cast<float*>(qq + ((hd + 15) & ~15));
+    int16_t* vl = reinterpret_cast<int16_t*>(sc + SMAX);
     const int tok = blockIdx.x / n_h, h = blockIdx.x - tok * n_h, pos = pos0 + tok;
     const int kvh = h / (n_h / n_kv);
     const float* qr = qg + ((size_t)tok * n_h + h) * 2 * hd;
@@ -142,6 +150,7 @@ __global__ void __launch_bounds__(RT) k_attn(const float* __restrict__ q_norm, c
     const float sq = block_quant_i8(x, hd, qq, red);
     __syncthreads();
     const int nkeys = pos + 1, hw = hd / 4;
+    const bool keep = nkeys <= SMAX;
     const int* qw = reinterpret_cast<const int*>(qq);
     auto score = [&](int j) __attribute__((always_inline)) {
         const int* kw = reinterpret_cast<const int*>(kq + ((size_t)j * n_kv + kvh) * hd);
@@ -149,35 +158,45 @@ __global__ void __launch_bounds__(RT) k_attn(const float* __restrict__ q_norm, c
         for (int w = 0; w < hw; w++) dot = __builtin_amdgcn_sdot4(qw[w], kw[w], dot, false);
         return ((float)dot * sq) * sk[(size_t)j * n_kv + kvh];
     };
-    // pass 1: the max
+    // pass 1: the max (scores kept for pass 2 when they fit)
     float mx = -__builtin_inff();
-    for (int j = threadIdx.x; j < nkeys; j += RT) mx = fmax_spec(mx, score(j));
+    for (int j = threadIdx.x; j < nkeys; j += RT) {
+        const float sj = score(j);
+        if (keep) sc[j] = sj;
+        mx = fmax_spec(mx, sj);
+    }
     mx = wave_fmax(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
     mx = -__builtin_inff();
     for (int w = 0; w < RT / 64; w++) mx = fmax_spec(mx, red[w]);
-    // pass 2: fixed-point weights chunk by chunk; thread i < hd accumulates num_i (dims i, i + RT, ...)
+    // pass 2: fixed-point weights and the value rows of kc keys at a time; thread i < hd owns num_i (dims i, i + RT..)
     constexpr int MAXD = 4;                        // hd <= 1024
     long long num[MAXD] = {0, 0, 0, 0};
     long long den = 0;
-    for (int c0 = 0; c0 < nkeys; c0 += KC) {
-        const int nc = min(KC, nkeys - c0);
-        __syncthreads();                           // the previous chunk's weights are consumed
+    const int q4 = hd / 4;                         // 8-byte (4 x int16) pieces per value row
+    for (int c0 = 0; c0 < nkeys; c0 += kc) {
+        const int nc = min(kc, nkeys - c0);
+        __syncthreads();                           // the previous chunk's weights and values are consumed
         for (int jj = threadIdx.x; jj < nc; jj += RT) {
-            const int pq = (int)rint_(exp_f(score(c0 + jj) - mx) * 16777216.0f);   // 0 .. 2^24
+            const float sj = keep ? sc[c0 + jj] : score(c0 + jj);
+            const int pq = (int)rint_(exp_f(sj - mx) * 16777216.0f);   // 0 .. 2^24
             pqs[jj] = pq;
             den += pq;
+        }
+        for (int e = threadIdx.x; e < nc * q4; e += RT) {
+            const int jj = e / q4, w = e - jj * q4;
+            const uint2 v4 = *reinterpret_cast<const uint2*>(vq + ((size_t)(c0 + jj) * n_kv + kvh) * hd + 4 * w);
+            *reinterpret_cast<uint2*>(vl + jj * hd + 4 * w) = v4;
         }
         __syncthreads();
 #pragma unroll
         for (int d = 0; d < MAXD; d++) {
             const int i = threadIdx.x + d * RT;
             if (i < hd) {
-                const int16_t* vc = vq + ((size_t)c0 * n_kv + kvh) * hd + i;
-                long long a = num[d];
-                for (int jj = 0; jj < nc; jj++) a += (long long)pqs[jj] * (long long)vc[(size_t)jj * n_kv * hd];
-                num[d] = a;
+                long long acc = num[d];
+                for (int jj = 0; jj < nc; jj++) acc += (long long)pqs[jj] * (long long)vl[jj * hd + i];
+                num[d] = acc;
             }
         }
     }
@@ -408,12 +427,15 @@ void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float*
     if (pos0 < 0 || (long long)pos0 + M > kv->capacity) DET_FAIL("det_attention: positions %d..%d exceed the cache of %d", pos0, pos0 + M - 1, kv->capacity);
     int p = 1;
     while (p < hd) p <<= 1;
-    const size_t lds = ((size_t)hd + p + p / 2 + 1) * 4 + (size_t)hd;
-    k_attn_kv<<<M * n_kv, RT, lds, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, rope_cos, rope_sin,
-                                         rot / 2, eps, pos0, n_kv, hd);
+    const size_t lds_kv = ((size_t)hd + p + p / 2) * 4;
+    k_attn_kv<<<M * n_kv, RT, lds_kv, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, rope_cos, rope_sin,
+                                            rot / 2, eps, pos0, n_kv, hd);
     DET_CHECK(hipGetLastError());
+    const int kc = std::min(256, 8192 / hd);       // keys per value chunk: 16 KB of int16 rows
+    const size_t lds = ((size_t)hd + p + p / 2 + 4) * 4 + (((size_t)hd + 15) & ~(size_t)15) + (size_t)SMAX * 4 +
+                       (size_t)kc * hd * 2;
     k_attn<<<M * n_h, RT, lds, st>>>(L->q_norm, L->v_scale, kv->kq, kv->sk, kv->vq, qg, rope_cos, rope_sin, rot / 2, eps,
-                                     pos0, n_h, n_kv, hd, o);
+                                     pos0, n_h, n_kv, hd, kc, o);
     DET_CHECK(hipGetLastError());
 }
 
