@@ -119,4 +119,24 @@ __device__ __forceinline__ float sigmoid_f(float x) {
 }
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
+// DPP lane exchange within a row of 16 lanes (ctrl: quad_perm 0xB1 = lane ^ 1, 0x4E = lane ^ 2; 0x141 row_half_mirror
+// = lane 7 - i of its 8; 0x140 row_mirror = lane 15 - i of its 16)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// Sum of the R adjacent lanes' subtree values (R = 1, 2, 4, 8 or 16, groups aligned to R), every lane of the group
+// receiving it, added in the balanced tree's order: pairs of lanes, then pairs of pairs, ...  Each level adds the
+// lower aligned half's value and the upper one's; fp32 addition commutes, so both halves compute the same sum.
+// After level 2 a quad holds one value, so the half-mirror partner holds the other quad's; likewise the mirror
+// partner after level 3.
+template <int R>
+__device__ __forceinline__ float lane_tree_sum(float v) {
+    if (R >= 2) v = v + dpp_f<0xB1>(v);
+    if (R >= 4) v = v + dpp_f<0x4E>(v);
+    if (R >= 8) v = v + dpp_f<0x141>(v);
+    if (R >= 16) v = v + dpp_f<0x140>(v);
+    return v;
+}
+
 } // namespace det

@@ -295,68 +295,106 @@ __device__ __forceinline__ float reg_tree(float* v) {
 
 // The recurrence of one v head over the M tokens in order (spec/layers.rs:90-130).  Column j of S[h] (dk rows)
 // is split over R adjacent lanes, lane r holding rows RB r .. RB r + RB - 1 (dk = R RB, a power of two), so a
-// column's treesum is the lane's subtree, then log2(R) shuffle levels that add the aligned subtrees in tree order
-// (pairs, then pairs of pairs; fp32 addition commutes).  The columns evolve independently, so a head's dv columns
-// are spread over blocks of CW columns (grid y), one workgroup each.  Every TC tokens a workgroup stages their k, q
-// (of the head's k head), its columns' v, beta and decay in LDS with one burst of loads, so the token loop itself
-// reads only LDS.
+// column's treesum is the lane's subtree, then log2(R) DPP levels that add the aligned subtrees in tree order
+// (lane_tree_sum).  The columns evolve independently, so a head's dv columns are spread over blocks of
+// CW = GT / R columns (grid y), one workgroup of GT threads each.  Tokens come in chunks of TC: a chunk's k, q (of
+// the head's k head), its columns' v, beta and decay are loaded into registers while the previous chunk is
+// computed from LDS, then written to the other of two LDS buffers (one barrier per chunk).  Inside a chunk the
+// next token's operands are read from LDS before the current token is computed.
+constexpr int GT = 256, GTC = 32;
 template <int RB, int R>
-__global__ void __launch_bounds__(1024) k_gdn_rec(float* __restrict__ S, const float* __restrict__ qb,
-                                                  const float* __restrict__ kb, const float* __restrict__ y,
-                                                  const float* __restrict__ bd, int M, int n_k, int n_v, int dv, int cd,
-                                                  int CW, float* __restrict__ ob) {
-    constexpr int DK = R * RB, TC = 32;
+__global__ void __launch_bounds__(GT) k_gdn_rec(float* __restrict__ S, const float* __restrict__ qb,
+                                                const float* __restrict__ kb, const float* __restrict__ y,
+                                                const float* __restrict__ bd, int M, int n_k, int n_v, int dv, int cd,
+                                                float* __restrict__ ob) {
+    constexpr int DK = R * RB, TC = GTC, CW = GT / R;
+    constexpr int LK = (TC * DK + GT - 1) / GT, LV = (TC * CW + GT - 1) / GT;
+    constexpr int BUF = 2 * TC * DK + TC * CW + 2 * TC;           // floats of one buffer: k, q, v, (beta, decay)
     extern __shared__ float sm[];
-    float* ks = sm;                       // [TC][DK]
-    float* qs = ks + TC * DK;             // [TC][DK]
-    float* bt = qs + TC * DK;             // [TC][2] beta, decay
-    float* vs = bt + 2 * TC;              // [TC][CW] v of this block's columns
-    const int h = blockIdx.x, kh = h / (n_v / n_k), j0 = blockIdx.y * CW;
-    const int jl = threadIdx.x / R, r = threadIdx.x % R, j = j0 + jl;
-    const bool live = jl < CW && j < dv;
+    const int h = blockIdx.x, kh = h / (n_v / n_k), j0 = blockIdx.y * CW, tid = threadIdx.x;
+    const int jl = tid / R, r = tid % R, j = j0 + jl;
+    const bool live = j < dv;
     float col[RB];
     float* Sh = S + (size_t)h * DK * dv;
 #pragma unroll
     for (int i = 0; i < RB; i++) col[i] = live ? Sh[(size_t)(r * RB + i) * dv + j] : 0.0f;
     const size_t vbase = (size_t)2 * n_k * DK + (size_t)h * dv;      // v of head h inside a token's conv outputs
+    float rk[LK], rq[LK], rv[LV], rb = 0.0f;
+    auto load = [&](int c0) __attribute__((always_inline)) {
+        const int nt = min(TC, M - c0);
+#pragma unroll
+        for (int u = 0; u < LK; u++) {
+            const int e = tid + u * GT, tt = e / DK, i = e - tt * DK;
+            const size_t src = ((size_t)(c0 + tt) * n_k + kh) * DK + i;
+            rk[u] = e < nt * DK ? kb[src] : 0.0f;
+            rq[u] = e < nt * DK ? qb[src] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < LV; u++) {
+            const int e = tid + u * GT, tt = e / CW, jj = e - tt * CW;
+            rv[u] = e < nt * CW && j0 + jj < dv ? y[(size_t)(c0 + tt) * cd + vbase + j0 + jj] : 0.0f;
+        }
+        if (tid < 2 * nt) rb = bd[2 * ((size_t)(c0 + tid / 2) * n_v + h) + (tid & 1)];
+    };
+    auto store = [&](float* buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < LK; u++) {
+            const int e = tid + u * GT;
+            if (e < TC * DK) { buf[e] = rk[u]; buf[TC * DK + e] = rq[u]; }
+        }
+#pragma unroll
+        for (int u = 0; u < LV; u++) {
+            const int e = tid + u * GT;
+            if (e < TC * CW) buf[2 * TC * DK + e] = rv[u];
+        }
+        if (tid < 2 * TC) buf[2 * TC * DK + TC * CW + tid] = rb;
+    };
+    load(0);
+    store(sm);
+    __syncthreads();
+    int cur = 0;
     for (int c0 = 0; c0 < M; c0 += TC) {
         const int nt = min(TC, M - c0);
-        __syncthreads();                                            // the previous chunk is consumed
-        for (int e = threadIdx.x; e < nt * DK; e += blockDim.x) {
-            const int tt = e / DK, i = e - tt * DK;
-            const size_t src = ((size_t)(c0 + tt) * n_k + kh) * DK + i;
-            ks[e] = kb[src];
-            qs[e] = qb[src];
-        }
-        for (int e = threadIdx.x; e < nt * CW; e += blockDim.x) {
-            const int tt = e / CW, jj = e - tt * CW;
-            vs[e] = j0 + jj < dv ? y[(size_t)(c0 + tt) * cd + vbase + j0 + jj] : 0.0f;
-        }
-        for (int e = threadIdx.x; e < 2 * nt; e += blockDim.x) bt[e] = bd[2 * ((size_t)(c0 + e / 2) * n_v + h) + (e & 1)];
-        __syncthreads();
+        const bool more = c0 + TC < M;
+        if (more) load(c0 + TC);
+        const float* ks = sm + cur * BUF;
+        const float* qs = ks + TC * DK;
+        const float* vs = qs + TC * DK;
+        const float* bt = vs + TC * CW;
+        float kc[RB], qc[RB], beta, decay, vj;
+        auto fetch = [&](int tt, float* kd, float* qd, float& be, float& de, float& vv) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < RB; i++) { kd[i] = ks[tt * DK + r * RB + i]; qd[i] = qs[tt * DK + r * RB + i]; }
+            be = bt[2 * tt];
+            de = bt[2 * tt + 1];
+            vv = vs[tt * CW + jl];
+        };
+        fetch(0, kc, qc, beta, decay, vj);
         for (int tt = 0; tt < nt; tt++) {
-            const float* kt = ks + tt * DK + r * RB;
-            const float* qt = qs + tt * DK + r * RB;
-            const float beta = bt[2 * tt], decay = bt[2 * tt + 1];
-            const float vj = live ? vs[tt * CW + jl] : 0.0f;
+            float kn[RB], qn[RB], bn, dn, vn;
+            fetch(min(tt + 1, nt - 1), kn, qn, bn, dn, vn);
             float p[RB];
 #pragma unroll
             for (int i = 0; i < RB; i++) col[i] = col[i] * decay;
 #pragma unroll
-            for (int i = 0; i < RB; i++) p[i] = col[i] * kt[i];
-            float kv = reg_tree<RB>(p);
-#pragma unroll
-            for (int o = 1; o < R; o <<= 1) kv = kv + __shfl_xor(kv, o, 64);
+            for (int i = 0; i < RB; i++) p[i] = col[i] * kc[i];
+            const float kv = lane_tree_sum<R>(reg_tree<RB>(p));
             const float delta = (vj - kv) * beta;
 #pragma unroll
-            for (int i = 0; i < RB; i++) col[i] = col[i] + (kt[i] * delta);
+            for (int i = 0; i < RB; i++) col[i] = col[i] + (kc[i] * delta);
 #pragma unroll
-            for (int i = 0; i < RB; i++) p[i] = col[i] * qt[i];
-            float oj = reg_tree<RB>(p);
-#pragma unroll
-            for (int o = 1; o < R; o <<= 1) oj = oj + __shfl_xor(oj, o, 64);
+            for (int i = 0; i < RB; i++) p[i] = col[i] * qc[i];
+            const float oj = lane_tree_sum<R>(reg_tree<RB>(p));
             if (live && r == 0) ob[((size_t)(c0 + tt) * n_v + h) * dv + j] = oj;
+#pragma unroll
+            for (int i = 0; i < RB; i++) { kc[i] = kn[i]; qc[i] = qn[i]; }
+            beta = bn;
+            decay = dn;
+            vj = vn;
         }
+        if (more) store(sm + (cur ^ 1) * BUF);
+        __syncthreads();
+        cur ^= 1;
     }
     if (live) {
 #pragma unroll
@@ -464,21 +502,24 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
     while (p < dk) p <<= 1;
     k_gdn_prep<<<M * n_k, RT, ((size_t)dk + p + p / 2) * 4, st>>>(y, L->A, L->dt_bias, a, b, eps, n_k, n_v, dk, cd, qb, kb, bd);
     DET_CHECK(hipGetLastError());
-    // lanes per column: 8 (4 when dk < 8); blocks of CW = 16 columns, one workgroup each (grid y)
-    const int R = dk >= 8 ? 8 : 4, CW = dv < 16 ? dv : 16, CB = (dv + CW - 1) / CW;
-    const int threads = ((CW * R + 63) / 64) * 64;
-    const size_t rl = ((size_t)2 * 32 * dk + 2 * 32 + (size_t)32 * CW) * sizeof(float);
-    const dim3 grid(n_v, CB);
-    if (R == 8) {
-        switch (dk / 8) {
-        case 1: k_gdn_rec<1, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
-        case 2: k_gdn_rec<2, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
-        case 4: k_gdn_rec<4, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
-        case 8: k_gdn_rec<8, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
-        default: k_gdn_rec<16, 8><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob); break;
-        }
-    } else {
-        k_gdn_rec<1, 4><<<grid, threads, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, CW, ob);
+    // lanes per column: 16 (dk when dk < 16); blocks of GT / R columns, one workgroup each (grid y)
+    const int R = dk < 16 ? dk : 16, CW = GT / R;
+    const dim3 grid(n_v, (dv + CW - 1) / CW);
+    const size_t rl = (size_t)2 * (2 * GTC * dk + GTC * CW + 2 * GTC) * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        const void* fs[] = {(const void*)k_gdn_rec<1, 4>, (const void*)k_gdn_rec<1, 8>, (const void*)k_gdn_rec<1, 16>,
+                            (const void*)k_gdn_rec<2, 16>, (const void*)k_gdn_rec<4, 16>, (const void*)k_gdn_rec<8, 16>};
+        for (const void* f : fs) DET_CHECK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+        attr = true;
+    }
+    switch (dk) {
+    case 4: k_gdn_rec<1, 4><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 8: k_gdn_rec<1, 8><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 16: k_gdn_rec<1, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 32: k_gdn_rec<2, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 64: k_gdn_rec<4, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    default: k_gdn_rec<8, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
     }
     DET_CHECK(hipGetLastError());
     int pv = 1;

@@ -107,12 +107,14 @@ def check_gdn(n_k, n_v, dk, dv, steps, seed):
 
 
 def test_gdn_4b_shape_prefill_then_decode():
-    check_gdn(16, 32, 128, 128, [19, 1, 1, 2], seed=4)
+    check_gdn(16, 32, 128, 128, [19, 1, 70, 1, 2], seed=4)
 
 
-@pytest.mark.parametrize('n_k,n_v,dk,dv', [(1, 2, 4, 4), (2, 4, 8, 16), (1, 1, 32, 24)])
+@pytest.mark.parametrize('n_k,n_v,dk,dv', [(1, 2, 4, 4), (2, 4, 8, 16), (1, 2, 16, 8), (1, 1, 32, 24),
+                                           (2, 2, 64, 40), (1, 1, 128, 20)])
 def test_gdn_small_shapes(n_k, n_v, dk, dv):
-    check_gdn(n_k, n_v, dk, dv, [1, 2, 5, 1], seed=5)
+    # 33 and 64 tokens span two token chunks of the recurrence (a partial and a full second one)
+    check_gdn(n_k, n_v, dk, dv, [1, 2, 5, 33, 64, 1], seed=5)
 
 
 @pytest.mark.parametrize('V', [1, 5, 1000, 248320])
