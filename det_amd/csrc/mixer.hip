@@ -15,7 +15,6 @@ using namespace det;
 namespace {
 
 constexpr int RT = 256;          // threads of the row kernels
-constexpr int KC = 1024;         // keys per chunk of the attention's second pass
 
 __device__ __forceinline__ int p2(int n) { int p = 1; while (p < n) p <<= 1; return p; }
 
@@ -112,34 +111,73 @@ __global__ void __launch_bounds__(RT) k_attn_kv(const float* __restrict__ k_norm
     }
 }
 
-// One workgroup per (token, head): q -> rmsnorm(q_norm) -> rope -> * 1/sqrt(hd) -> quant_act_i8 (qq, sq); keys
-// 0 .. pos of kv head h / rep: s_j = (f32(dot(qq, kq_j)) * sq) * sk_j, mx = fmax fold, pq_j = rint(exp(s_j - mx)
-// * 2^24) as int64, den = sum pq_j, num_i = sum pq_j vq_j[i] (exact, order-free), o_i = ((f32(num_i) / f32(den)) *
-// v_scale) * sigmoid(gate_i) (spec/layers.rs:24-69).  The max pass keeps the scores in LDS (up to SMAX keys; longer
-// rows recompute them); the weight pass walks the keys in chunks of kc whose value rows are staged in LDS by
-// coalesced loads, so the numerators read LDS only.
-// Dynamic LDS: x[hd], tree s[p], t[p / 2] floats, qq[hd] bytes, scores sc[SMAX], values vl[kc][hd] int16.
-constexpr int SMAX = 2048;
-__global__ void __launch_bounds__(RT) k_attn(const float* __restrict__ q_norm, const float* __restrict__ v_scale,
-                                             const int8_t* __restrict__ kq, const float* __restrict__ sk,
-                                             const int16_t* __restrict__ vq, const float* __restrict__ qg,
-                                             const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
-                                             int half, float eps, int pos0, int n_h, int n_kv, int hd, int kc,
-                                             float* __restrict__ o) {
+// The attention of a token and head over keys 0 .. pos of kv head h / rep (spec/layers.rs:24-69):
+// s_j = (f32(dot(qq, kq_j)) * sq) * sk_j, mx = fmax fold of the s_j, pq_j = rint(exp(s_j - mx) * 2^24) as an
+// integer, den = sum pq_j, num_i = sum pq_j vq_j[i], o_i = ((f32(num_i) / f32(den)) * v_scale) * sigmoid(gate_i).
+// The max is order-free and the sums are exact integers, so the keys are split into chunks of CK, one workgroup
+// each (grid x = chunk, grid y = token * n_h + head), and the chunks meet through device atomics:
+//   k_attn_q   q -> rmsnorm(q_norm) -> rope -> * 1/sqrt(hd) -> quant_act_i8 into scratch; clears the head's
+//              max, den and num (so no memset is needed and the launches can be captured);
+//   k_attn_max the chunk's scores and their max, merged by atomicMax on an order-preserving integer image;
+//   k_attn_acc the chunk's scores again (same integers, same fp32 ops), its pq_j, and the chunk's den and num
+//              partials added by int64 atomics;
+//   k_attn_fin the output.
+// A score takes 16 lanes: lane l reads words l, l + 16, ... of the key row (coalesced) into v_dot4 sums, and the
+// 16 partial sums meet by DPP exchanges (integers: any order).
+struct AttnScratch {
+    int8_t* qq;       // [M][n_h][hd]
+    float* sq;        // [M][n_h]
+    unsigned* mxo;    // [M][n_h] order-preserving image of the max
+    long long* den;   // [M][n_h]
+    long long* num;   // [M][n_h][hd]
+    size_t bytes;
+};
+__host__ __device__ inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+inline AttnScratch attn_layout(void* base, int M, int n_h, int hd) {
+    AttnScratch S{};
+    const size_t r = (size_t)M * n_h;
+    char* p = static_cast<char*>(base);
+    size_t off = 0;
+    S.qq = reinterpret_cast<int8_t*>(p + off);     off += al256(r * hd);
+    S.sq = reinterpret_cast<float*>(p + off);      off += al256(r * 4);
+    S.mxo = reinterpret_cast<unsigned*>(p + off);  off += al256(r * 4);
+    S.den = reinterpret_cast<long long*>(p + off); off += al256(r * 8);
+    S.num = reinterpret_cast<long long*>(p + off); off += al256(r * hd * 8);
+    S.bytes = off;
+    return S;
+}
+// fp32 total order of fmax_spec (-0 below +0; every NaN above everything, as one canonical NaN) as unsigned
+// integers, 0 below every value
+__device__ __forceinline__ unsigned f2ord(float f) {
+    if (__builtin_isnan(f)) return 0xffffffffu;
+    const unsigned u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ord2f(unsigned u) {
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+__device__ __forceinline__ int sum16(int v) {       // every lane of an aligned 16-lane row gets the row's sum
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    v += dpp_i<0x141>(v);
+    v += dpp_i<0x140>(v);
+    return v;
+}
+constexpr int AQW = 16;     // max words (4 codes each) per lane of a score: hd <= 1024
+
+__global__ void __launch_bounds__(RT) k_attn_q(const float* __restrict__ q_norm, const float* __restrict__ qg,
+                                               const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+                                               int half, float eps, int pos0, int n_h, int hd, AttnScratch S) {
     extern __shared__ float lds[];
     __shared__ float red[RT / 64];
-    __shared__ int pqs[256];
-    __shared__ long long dens[RT / 64];
     const int p = p2(hd);
     float* x = lds;
     float* s = x + hd;
     float* t = s + p;
-    int8_t* qq = reinterpret_cast<int8_t*>(t + p / 2 + 4);
-    float* sc = reinterpret_cast<float*>(qq + ((hd + 15) & ~15));
-    int16_t* vl = reinterpret_cast<int16_t*>(sc + SMAX);
-    const int tok = blockIdx.x / n_h, h = blockIdx.x - tok * n_h, pos = pos0 + tok;
-    const int kvh = h / (n_h / n_kv);
-    const float* qr = qg + ((size_t)tok * n_h + h) * 2 * hd;
+    const int row = blockIdx.x, tok = row / n_h, pos = pos0 + tok;
+    const float* qr = qg + (size_t)row * 2 * hd;
     for (int i = threadIdx.x; i < hd; i += RT) x[i] = qr[i];
     __syncthreads();
     block_rmsnorm(x, hd, q_norm, eps, s, t);
@@ -147,73 +185,101 @@ __global__ void __launch_bounds__(RT) k_attn(const float* __restrict__ q_norm, c
     const float qscale = 1.0f / __builtin_sqrtf((float)hd);
     for (int i = threadIdx.x; i < hd; i += RT) x[i] = x[i] * qscale;
     __syncthreads();
-    const float sq = block_quant_i8(x, hd, qq, red);
-    __syncthreads();
-    const int nkeys = pos + 1, hw = hd / 4;
-    const bool keep = nkeys <= SMAX;
-    const int* qw = reinterpret_cast<const int*>(qq);
-    auto score = [&](int j) __attribute__((always_inline)) {
-        const int* kw = reinterpret_cast<const int*>(kq + ((size_t)j * n_kv + kvh) * hd);
-        int dot = 0;
-        for (int w = 0; w < hw; w++) dot = __builtin_amdgcn_sdot4(qw[w], kw[w], dot, false);
-        return ((float)dot * sq) * sk[(size_t)j * n_kv + kvh];
-    };
-    // pass 1: the max (scores kept for pass 2 when they fit)
-    float mx = -__builtin_inff();
-    for (int j = threadIdx.x; j < nkeys; j += RT) {
-        const float sj = score(j);
-        if (keep) sc[j] = sj;
-        mx = fmax_spec(mx, sj);
+    const float sq = block_quant_i8(x, hd, S.qq + (size_t)row * hd, red);
+    for (int i = threadIdx.x; i < hd; i += RT) S.num[(size_t)row * hd + i] = 0;
+    if (threadIdx.x == 0) {
+        S.sq[row] = sq;
+        S.mxo[row] = 0u;
+        S.den[row] = 0;
     }
+}
+
+// scores of the chunk's keys for this thread's 16-lane row: calls f(key, score) on lane 0 of the row for every key
+template <class F>
+__device__ __forceinline__ void chunk_scores(const int8_t* __restrict__ kq, const float* __restrict__ sk,
+                                             const AttnScratch& S, int row, int kvh, int n_kv, int hd, int j0, int j1,
+                                             F&& f) {
+    const int l16 = threadIdx.x & 15, kslot = threadIdx.x >> 4, hw = hd / 4;
+    const int* qw = reinterpret_cast<const int*>(S.qq + (size_t)row * hd);
+    int q[AQW];
+#pragma unroll
+    for (int u = 0; u < AQW; u++) q[u] = l16 + 16 * u < hw ? qw[l16 + 16 * u] : 0;
+    const float sq = S.sq[row];
+    for (int jb = j0; jb < j1; jb += RT / 16) {          // uniform trip count: every row takes part in the DPP sums
+        const int j = jb + kslot;
+        int dot = 0;
+        if (j < j1) {
+            const int* kw = reinterpret_cast<const int*>(kq + ((size_t)j * n_kv + kvh) * hd);
+#pragma unroll
+            for (int u = 0; u < AQW; u++)
+                if (l16 + 16 * u < hw) dot = __builtin_amdgcn_sdot4(q[u], kw[l16 + 16 * u], dot, false);
+        }
+        dot = sum16(dot);
+        if (j < j1 && l16 == 0) f(j, ((float)dot * sq) * sk[(size_t)j * n_kv + kvh]);
+    }
+}
+
+template <int CK>
+__global__ void __launch_bounds__(RT) k_attn_max(const int8_t* __restrict__ kq, const float* __restrict__ sk, int pos0,
+                                                 int n_h, int n_kv, int hd, AttnScratch S) {
+    __shared__ float red[RT / 64];
+    const int row = blockIdx.y, tok = row / n_h, h = row - tok * n_h, kvh = h / (n_h / n_kv);
+    const int nkeys = pos0 + tok + 1, j0 = blockIdx.x * CK;
+    if (j0 >= nkeys) return;                              // uniform: the whole workgroup leaves
+    float mx = -__builtin_inff();
+    chunk_scores(kq, sk, S, row, kvh, n_kv, hd, j0, min(j0 + CK, nkeys), [&](int, float sj) { mx = fmax_spec(mx, sj); });
     mx = wave_fmax(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    mx = -__builtin_inff();
-    for (int w = 0; w < RT / 64; w++) mx = fmax_spec(mx, red[w]);
-    // pass 2: fixed-point weights and the value rows of kc keys at a time; thread i < hd owns num_i (dims i, i + RT..)
-    constexpr int MAXD = 4;                        // hd <= 1024
-    long long num[MAXD] = {0, 0, 0, 0};
-    long long den = 0;
-    const int q4 = hd / 4;                         // 8-byte (4 x int16) pieces per value row
-    for (int c0 = 0; c0 < nkeys; c0 += kc) {
-        const int nc = min(kc, nkeys - c0);
-        __syncthreads();                           // the previous chunk's weights and values are consumed
-        for (int jj = threadIdx.x; jj < nc; jj += RT) {
-            const float sj = keep ? sc[c0 + jj] : score(c0 + jj);
-            const int pq = (int)rint_(exp_f(sj - mx) * 16777216.0f);   // 0 .. 2^24
-            pqs[jj] = pq;
-            den += pq;
-        }
-        for (int e = threadIdx.x; e < nc * q4; e += RT) {
-            const int jj = e / q4, w = e - jj * q4;
-            const uint2 v4 = *reinterpret_cast<const uint2*>(vq + ((size_t)(c0 + jj) * n_kv + kvh) * hd + 4 * w);
-            *reinterpret_cast<uint2*>(vl + jj * hd + 4 * w) = v4;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int d = 0; d < MAXD; d++) {
-            const int i = threadIdx.x + d * RT;
-            if (i < hd) {
-                long long acc = num[d];
-                for (int jj = 0; jj < nc; jj++) acc += (long long)pqs[jj] * (long long)vl[jj * hd + i];
-                num[d] = acc;
-            }
-        }
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < RT / 64; w++) mx = fmax_spec(mx, red[w]);
+        atomicMax(S.mxo + row, f2ord(mx));
     }
+}
+
+template <int CK>
+__global__ void __launch_bounds__(RT) k_attn_acc(const int8_t* __restrict__ kq, const float* __restrict__ sk,
+                                                 const int16_t* __restrict__ vq, int pos0, int n_h, int n_kv, int hd,
+                                                 AttnScratch S) {
+    __shared__ int pqs[CK];
+    __shared__ long long dens[RT / 64];
+    const int row = blockIdx.y, tok = row / n_h, h = row - tok * n_h, kvh = h / (n_h / n_kv);
+    const int nkeys = pos0 + tok + 1, j0 = blockIdx.x * CK;
+    if (j0 >= nkeys) return;
+    const int j1 = min(j0 + CK, nkeys);
+    const float mx = ord2f(S.mxo[row]);
+    long long den = 0;
+    chunk_scores(kq, sk, S, row, kvh, n_kv, hd, j0, j1, [&](int j, float sj) {
+        const int pq = (int)rint_(exp_f(sj - mx) * 16777216.0f);   // 0 .. 2^24
+        pqs[j - j0] = pq;
+        den += pq;
+    });
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off, 64);
     if ((threadIdx.x & 63) == 0) dens[threadIdx.x >> 6] = den;
     __syncthreads();
-    den = 0;
-    for (int w = 0; w < RT / 64; w++) den += dens[w];
-    const float fden = i64_to_f(den), vs = v_scale[kvh];
-    const float* gate = qr + hd;
-    float* oh = o + ((size_t)tok * n_h + h) * hd;
-#pragma unroll
-    for (int d = 0; d < MAXD; d++) {
-        const int i = threadIdx.x + d * RT;
-        if (i < hd) oh[i] = ((i64_to_f(num[d]) / fden) * vs) * sigmoid_f(gate[i]);
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < RT / 64; w++) den += dens[w];
+        atomicAdd(reinterpret_cast<unsigned long long*>(S.den + row), (unsigned long long)den);
     }
+    const int nc = j1 - j0;
+    const int16_t* vb = vq + ((size_t)j0 * n_kv + kvh) * hd;
+    const size_t vstride = (size_t)n_kv * hd;
+    for (int i = threadIdx.x; i < hd; i += RT) {
+        long long acc = 0;
+#pragma unroll 16
+        for (int jj = 0; jj < nc; jj++) acc += (long long)pqs[jj] * (long long)vb[jj * vstride + i];
+        atomicAdd(reinterpret_cast<unsigned long long*>(S.num + (size_t)row * hd + i), (unsigned long long)acc);
+    }
+}
+
+__global__ void __launch_bounds__(RT) k_attn_fin(const float* __restrict__ v_scale, const float* __restrict__ qg,
+                                                 int n_h, int n_kv, int hd, AttnScratch S, float* __restrict__ o) {
+    const int row = blockIdx.x, h = row % n_h, kvh = h / (n_h / n_kv);
+    const float fden = i64_to_f(S.den[row]), vs = v_scale[kvh];
+    const float* gate = qg + (size_t)row * 2 * hd + hd;
+    for (int i = threadIdx.x; i < hd; i += RT)
+        o[(size_t)row * hd + i] = ((i64_to_f(S.num[(size_t)row * hd + i]) / fden) * vs) * sigmoid_f(gate[i]);
 }
 
 // ------------------------------------------------------------------ Gated DeltaNet (cpu.rs:287-383)
@@ -452,28 +518,44 @@ size_t gdn_scratch_floats(int M, int n_k, int n_v, int dk, int dv) {
 
 extern "C" {
 
-size_t det_attn_scratch_bytes(int M, int n_h, int hd) { (void)M; (void)n_h; (void)hd; return 0; }
+size_t det_attn_scratch_bytes(int M, int n_h, int hd) {
+    return attn_layout(nullptr, M < 1 ? 1 : M, n_h < 1 ? 1 : n_h, hd < 4 ? 4 : hd).bytes;
+}
 
 void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float* qg, const float* k, const float* v,
                    const float* rope_cos, const float* rope_sin, int rot, float eps, int M, int pos0, int n_h, int n_kv,
                    int hd, float* o, void* scratch, hipStream_t st) {
-    (void)scratch;
     if (M < 1) return;
-    if (hd < 4 || hd > 1024 || hd % 4) DET_FAIL("det_attention: head_dim %d (multiple of 4, at most 1024)", hd);
+    if (hd < 4 || hd > 4 * 16 * AQW || hd % 4) DET_FAIL("det_attention: head_dim %d (multiple of 4, at most 1024)", hd);
     if (n_kv < 1 || n_h < n_kv || n_h % n_kv) DET_FAIL("det_attention: %d heads over %d kv heads", n_h, n_kv);
     if (rot < 0 || rot > hd || rot % 2) DET_FAIL("det_attention: rot %d for head_dim %d", rot, hd);
     if (pos0 < 0 || (long long)pos0 + M > kv->capacity) DET_FAIL("det_attention: positions %d..%d exceed the cache of %d", pos0, pos0 + M - 1, kv->capacity);
+    if (!scratch) DET_FAIL("det_attention: scratch of det_attn_scratch_bytes(M, n_h, hd) is required");
+    if ((long long)M * n_h > 65535) DET_FAIL("det_attention: %d tokens x %d heads exceed the grid", M, n_h);
     int p = 1;
     while (p < hd) p <<= 1;
-    const size_t lds_kv = ((size_t)hd + p + p / 2) * 4;
-    k_attn_kv<<<M * n_kv, RT, lds_kv, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, rope_cos, rope_sin,
-                                            rot / 2, eps, pos0, n_kv, hd);
+    const size_t lds_row = ((size_t)hd + p + p / 2) * 4;
+    k_attn_kv<<<M * n_kv, RT, lds_row, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, rope_cos, rope_sin,
+                                             rot / 2, eps, pos0, n_kv, hd);
     DET_CHECK(hipGetLastError());
-    const int kc = std::min(256, 8192 / hd);       // keys per value chunk: 16 KB of int16 rows
-    const size_t lds = ((size_t)hd + p + p / 2 + 4) * 4 + (((size_t)hd + 15) & ~(size_t)15) + (size_t)SMAX * 4 +
-                       (size_t)kc * hd * 2;
-    k_attn<<<M * n_h, RT, lds, st>>>(L->q_norm, L->v_scale, kv->kq, kv->sk, kv->vq, qg, rope_cos, rope_sin, rot / 2, eps,
-                                     pos0, n_h, n_kv, hd, kc, o);
+    const AttnScratch S = attn_layout(scratch, M, n_h, hd);
+    k_attn_q<<<M * n_h, RT, lds_row, st>>>(L->q_norm, qg, rope_cos, rope_sin, rot / 2, eps, pos0, n_h, hd, S);
+    DET_CHECK(hipGetLastError());
+    // chunks of 32 keys for a few tokens (a decode step: many workgroups per head), 256 for a batch
+    const int nkeys = pos0 + M;
+    if (M <= 4) {
+        const dim3 grid((nkeys + 31) / 32, M * n_h);
+        k_attn_max<32><<<grid, RT, 0, st>>>(kv->kq, kv->sk, pos0, n_h, n_kv, hd, S);
+        DET_CHECK(hipGetLastError());
+        k_attn_acc<32><<<grid, RT, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, n_h, n_kv, hd, S);
+    } else {
+        const dim3 grid((nkeys + 255) / 256, M * n_h);
+        k_attn_max<256><<<grid, RT, 0, st>>>(kv->kq, kv->sk, pos0, n_h, n_kv, hd, S);
+        DET_CHECK(hipGetLastError());
+        k_attn_acc<256><<<grid, RT, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, n_h, n_kv, hd, S);
+    }
+    DET_CHECK(hipGetLastError());
+    k_attn_fin<<<M * n_h, RT, 0, st>>>(L->v_scale, qg, n_h, n_kv, hd, S, o);
     DET_CHECK(hipGetLastError());
 }
 

@@ -59,6 +59,7 @@ struct det_model {
     int8_t *xq, *oq, *onq, *hq;
     uint16_t *mx, *mo, *mon, *mh;
     void* gdn_scratch = nullptr;
+    void* attn_scratch = nullptr;
     int* pick = nullptr;
     std::vector<float> host_x;
 
@@ -289,6 +290,7 @@ det_model* load(const std::string& path, int max_ctx, int max_batch) {
     m->logits = m->alloc<float>(c.vocab);
     m->pick = m->alloc<int>(1);
     m->gdn_scratch = m->alloc<uint8_t>(det_gdn_scratch_bytes(max_batch, n_k, n_v, dk, dv));
+    m->attn_scratch = m->alloc<uint8_t>(det_attn_scratch_bytes(max_batch, (int)m->c.n_heads, (int)m->c.head_dim));
     DET_CHECK(hipStreamSynchronize(m->st));
     return m.release();
 }
@@ -317,7 +319,7 @@ void forward_layers(det_model* m, int pos0, int t) {
         if (L.attn) {
             m->project(L.a.qkv, m->xq, m->sx, m->mx, t, {m->qg, m->k, m->v});
             det_attention(&L.a.layer, &L.a.kv, m->qg, m->k, m->v, m->rope_cos, m->rope_sin, (int)c.rot_dim, eps, t, pos0,
-                          n_h, n_kv, hd, m->o, nullptr, st);
+                          n_h, n_kv, hd, m->o, m->attn_scratch, st);
             det_quant(m->o, t, n_h * hd, m->oq, m->so, m->mo, st);
             det_gemm_ex(&L.a.o.lins[0].q, m->oq, m->so, m->mo, t, m->x, 1, 0, nullptr, nullptr, st);
         } else {

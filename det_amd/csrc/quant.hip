@@ -18,13 +18,35 @@ enum { MODE_QUANT = 0, MODE_RMSNORM = 1, MODE_SILU_MUL = 2 };
 
 __host__ __device__ __forceinline__ int p_of(int n) { int p = 1; while (p < n) p <<= 1; return p; }
 
+// order-free max over the wave: DPP exchanges inside rows of 16 lanes, then two lane shuffles
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmax_spec(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmax_spec(v, dpp_f<0xB1>(v));
+    v = fmax_spec(v, dpp_f<0x4E>(v));
+    v = fmax_spec(v, dpp_f<0x141>(v));
+    v = fmax_spec(v, dpp_f<0x140>(v));
+    v = fmax_spec(v, __shfl_xor(v, 16, 64));
+    return fmax_spec(v, __shfl_xor(v, 32, 64));
 }
 
-// dynamic LDS: v[n] fp32 (the row after its producer op), then for MODE_RMSNORM the tree buffers s[p], t[p/2]
+// balanced tree over the N values of r (adjacent pairs level by level)
+template <int N>
+__device__ __forceinline__ float tree_reg(float* r) {
+#pragma unroll
+    for (int w = N >> 1; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; i++) r[i] = r[2 * i] + r[2 * i + 1];
+    return r[0];
+}
+// the subtree of squares of v over the aligned leaves [i0, i0 + E) (leaves past n are +0)
+template <int E>
+__device__ __forceinline__ float sq_subtree(const float* v, int n, int i0) {
+    float r[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) r[i] = i0 + i < n ? v[i0 + i] * v[i0 + i] : 0.0f;
+    return tree_reg<E>(r);
+}
+
+// dynamic LDS: v[n] fp32 (the row after its producer op)
 template <int MODE, int QT>
 __global__ void __launch_bounds__(QT) k_quant(const float* __restrict__ a, const float* __restrict__ b, float eps, int n,
                                               float* __restrict__ y, int8_t* __restrict__ xq, float* __restrict__ sx,
@@ -37,34 +59,70 @@ __global__ void __launch_bounds__(QT) k_quant(const float* __restrict__ a, const
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const size_t off = (size_t)row * n;
 
-    for (int i = tid; i < n; i += QT) {
-        float x = a[off + i];
-        if (MODE == MODE_SILU_MUL) {
-            x = silu_f(x) * b[off + i];
-            if (y) y[off + i] = x;
+    // LB elements per thread are loaded before any is used, so their latencies overlap
+    constexpr int LB = 8;
+    for (int i0 = tid; i0 < n; i0 += LB * QT) {
+        float ra[LB], rb[LB];
+#pragma unroll
+        for (int u = 0; u < LB; u++) {
+            const int i = i0 + u * QT;
+            ra[u] = i < n ? a[off + i] : 0.0f;
+            if (MODE == MODE_SILU_MUL) rb[u] = i < n ? b[off + i] : 0.0f;
         }
-        v[i] = x;
+#pragma unroll
+        for (int u = 0; u < LB; u++) {
+            const int i = i0 + u * QT;
+            if (i < n) {
+                float x = ra[u];
+                if (MODE == MODE_SILU_MUL) {
+                    x = silu_f(x) * rb[u];
+                    if (y) y[off + i] = x;
+                }
+                v[i] = x;
+            }
+        }
     }
     if (MODE == MODE_RMSNORM) {
-        // spec/prim.rs:172-181: ss = treesum(x*x) over the row padded with +0 to p = next power of two
-        float* s = lds + n;            // ping-pong tree buffers s[p], t[p/2]
-        float* t = s + p_of(n);
-        const int p = p_of(n);
+        // spec/prim.rs:172-181: ss = treesum(x*x) over the row padded with +0 to p = next power of two.  The
+        // squares are >= +0, so the tree over max(p, QT) leaves (zeros past p) has the same root: its extra
+        // levels only add +0.  Thread t sums the aligned leaves [t E, t E + E) as a subtree, the wave's lanes
+        // combine theirs pairwise (DPP, then two shuffles), and the waves' subtrees meet in tree order.
+        const int p = p_of(n), E = p > QT ? p / QT : 1;
         __syncthreads();
-        for (int i = tid; i < p; i += QT) s[i] = i < n ? v[i] * v[i] : 0.0f;
-        for (int w = p >> 1; w >= 1; w >>= 1) {
-            __syncthreads();
-            for (int i = tid; i < w; i += QT) t[i] = s[2 * i] + s[2 * i + 1];
-            float* u = s; s = t; t = u;
+        float ts;
+        switch (E) {
+        case 1: ts = sq_subtree<1>(v, n, tid); break;
+        case 2: ts = sq_subtree<2>(v, n, tid * 2); break;
+        case 4: ts = sq_subtree<4>(v, n, tid * 4); break;
+        case 8: ts = sq_subtree<8>(v, n, tid * 8); break;
+        case 16: ts = sq_subtree<16>(v, n, tid * 16); break;
+        default: ts = sq_subtree<32>(v, n, tid * 32); break;
         }
+        ts = lane_tree_sum<16>(ts);
+        ts = ts + __shfl_xor(ts, 16, 64);
+        ts = ts + __shfl_xor(ts, 32, 64);
+        if (lane == 0) red[wv] = ts;
         __syncthreads();
-        const float ss = s[0];
+        float wsum[QW];
+#pragma unroll
+        for (int w = 0; w < QW; w++) wsum[w] = red[w];
+        const float ss = tree_reg<QW>(wsum);
+        __syncthreads();                                  // red is reused by the plain quantization below
         const float mean = ss / (float)n;
         const float inv = 1.0f / __builtin_sqrtf(mean + eps);
-        for (int i = tid; i < n; i += QT) {
-            const float t = (v[i] * inv) * b[i];
-            v[i] = t;
-            if (y) y[off + i] = t;
+        for (int i0 = tid; i0 < n; i0 += LB * QT) {
+            float rw[LB];
+#pragma unroll
+            for (int u = 0; u < LB; u++) rw[u] = i0 + u * QT < n ? b[i0 + u * QT] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < LB; u++) {
+                const int i = i0 + u * QT;
+                if (i < n) {
+                    const float t = (v[i] * inv) * rw[u];
+                    v[i] = t;
+                    if (y) y[off + i] = t;
+                }
+            }
         }
     }
     __syncthreads();
@@ -120,7 +178,7 @@ void launch(const float* a, const float* b, float eps, int M, int n, float* y, i
     int p = 1;
     while (p < n) p <<= 1;
     if (MODE == MODE_RMSNORM && p > 8192) DET_FAIL("%s: unsupported n=%d", who, n);
-    const size_t lds = (size_t)n * 4 + (MODE == MODE_RMSNORM ? (size_t)p * 6 : 0);
+    const size_t lds = (size_t)n * 4;
     if (lds > 150 * 1024) DET_FAIL("%s: row of n=%d does not fit in LDS", who, n);
     static bool attr = false;
     if (!attr) {

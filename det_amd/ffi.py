@@ -212,8 +212,9 @@ def test_prim(op, x, M, n):
 
 def attention(layer, kv, qg, k, v, rope_cos, rope_sin, rot, eps, M, pos0, n_h, n_kv, hd, o):
     """Backend::attention (backend.rs; cpu.rs:212-285) over det_attention.  layer: AttnLayer, kv: KvCache."""
+    scratch = Buf(lib().det_attn_scratch_bytes(M, n_h, hd), np.uint8)
     lib().det_attention(ctypes.byref(layer), ctypes.byref(kv), qg.ptr, k.ptr, v.ptr, rope_cos.ptr, rope_sin.ptr, rot,
-                        eps, M, pos0, n_h, n_kv, hd, o.ptr, None, None)
+                        eps, M, pos0, n_h, n_kv, hd, o.ptr, scratch.ptr, None)
 
 
 def gdn(layer, state, qkv, z, a, b, eps, M, n_k, n_v, dk, dv, on, scratch):

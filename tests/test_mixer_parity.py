@@ -66,6 +66,11 @@ def test_attention_4b_shape_prefill_then_decode():
     check_attention(16, 4, 256, 64, [37, 1, 1, 5], 64, seed=1)
 
 
+def test_attention_4b_shape_decode_over_many_key_chunks():
+    """Decode steps whose keys span many 32-key chunks, and batches spanning 256-key chunks."""
+    check_attention(16, 4, 256, 64, [300, 1, 1, 3, 200, 1], 600, seed=6)
+
+
 def test_attention_long_prefill_chunks():
     """More than one 1024-key chunk in the weight pass, and the last cache row."""
     check_attention(2, 1, 64, 16, [1100, 1], 1101, seed=2)
