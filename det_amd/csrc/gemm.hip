@@ -243,6 +243,14 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
     long long acc[MP];
 #pragma unroll
     for (int t = 0; t < MP; t++) acc[t] = 0;
+    // the epilogue's row scales and token scales, loaded now so that their latency hides under the weight stream
+    float csr[MP], sxr[MP];
+#pragma unroll
+    for (int r = 0; r < MP; r++) {
+        const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
+        csr[r] = n < N ? cs[n] : 0.0f;
+        sxr[r] = t < M ? sx[t] : 0.0f;
+    }
     // matrix-core path: the token whose activations this lane feeds into A (-1: none)
     const int ai = lane & 31;
     int atok = (lane < 32) ? (ai < MP ? ai : -1) : (ai >= MP && ai < 2 * MP ? ai - MP : -1);
@@ -325,7 +333,7 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
 #pragma unroll
         for (int r = 0; r < MP; r++) {
             const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
-            if (t < M && n < N) out.store(N, t, n, (i64_to_f(acc[r]) * cs[n]) * sx[t]);
+            if (t < M && n < N) out.store(N, t, n, (i64_to_f(acc[r]) * csr[r]) * sxr[r]);
         }
         return;
     }
@@ -368,7 +376,7 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
 #pragma unroll
     for (int r = 0; r < MP; r++) {
         const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
-        if (r % S == wv && t < M && n < N) out.store(N, t, n, (i64_to_f(tot[r]) * cs[n]) * sx[t]);
+        if (r % S == wv && t < M && n < N) out.store(N, t, n, (i64_to_f(tot[r]) * csr[r]) * sxr[r]);
     }
 }
 

@@ -482,32 +482,106 @@ __global__ void __launch_bounds__(RT) k_gdn_out(const float* __restrict__ ob, co
     for (int i = threadIdx.x; i < dv; i += RT) on[base + i] = x[i] * silu_f(z[base + i]);
 }
 
-// ------------------------------------------------------------------ argmax (spec/sample.rs:6-14)
-// the first index of the largest value: every thread scans its indices in increasing order with a strict >, the
-// block keeps the larger value and, on equal values, the lower index
-__global__ void __launch_bounds__(1024) k_argmax(const float* __restrict__ logits, int V, int* __restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    const float* l = logits + (size_t)blockIdx.x * V;
-    float best = -__builtin_inff();
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < V; i += blockDim.x)
-        if (idx == 0x7fffffff || l[i] > best) { best = l[i]; idx = i; }
-    auto better = [](float v, int i, float w, int k) { return k != 0x7fffffff && (i == 0x7fffffff || w > v || (w == v && k < i)); };
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float w = __shfl_xor(best, off, 64);
-        const int k = __shfl_xor(idx, off, 64);
-        if (better(best, idx, w, k)) { best = w; idx = k; }
+// ---- one decode token (M = 1): the input stage in one launch instead of three
+// k_gdn_in1: one workgroup per k head: conv + silu of its q and k channels and of its rep v heads' v channels, the
+// conv window update of those channels (each channel belongs to one workgroup, so its thread reads the old rows
+// before writing the new ones), l2norm of q (times QSCALE) and k, and beta / decay of the rep v heads.  The same
+// operations, in the same order, as k_gdn_conv, k_gdn_conv_state and k_gdn_prep.
+__global__ void __launch_bounds__(RT) k_gdn_in1(const float* __restrict__ conv_w, float* __restrict__ conv_state,
+                                                const float* __restrict__ qkv, const float* __restrict__ A,
+                                                const float* __restrict__ dt_bias, const float* __restrict__ a,
+                                                const float* __restrict__ b, float eps, int n_k, int n_v, int dk, int dv,
+                                                int cd, float* __restrict__ y, float* __restrict__ qb,
+                                                float* __restrict__ kb, float* __restrict__ bd) {
+    extern __shared__ float lds[];
+    const int p = p2(dk);
+    float* x = lds;                  // conv q [dk], then conv k [dk]
+    float* s = x + 2 * dk;
+    float* t = s + p;
+    const int kh = blockIdx.x, rep = n_v / n_k, nch = 2 * dk + rep * dv;
+    for (int e = threadIdx.x; e < nch; e += RT) {
+        const int c = e < dk ? kh * dk + e
+                    : e < 2 * dk ? n_k * dk + kh * dk + (e - dk)
+                    : 2 * n_k * dk + kh * rep * dv + (e - 2 * dk);
+        const float o0 = conv_state[c], o1 = conv_state[(size_t)cd + c], o2 = conv_state[2 * (size_t)cd + c];
+        const float in = qkv[c];
+        const float* w = conv_w + (size_t)c * 4;
+        float acc = (w[0] * o0) + (w[1] * o1);       // spec/layers.rs:132-138
+        acc = acc + (w[2] * o2);
+        acc = acc + (w[3] * in);
+        const float v = silu_f(acc);
+        if (e < 2 * dk) x[e] = v;
+        else y[c] = v;
+        conv_state[c] = o1;
+        conv_state[(size_t)cd + c] = o2;
+        conv_state[2 * (size_t)cd + c] = in;
     }
-    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = idx; }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++)      // lane 0 already holds wave 0's pick
-            if (better(best, idx, bv[w], bi[w])) { best = bv[w]; idx = bi[w]; }
-        out[blockIdx.x] = idx == 0x7fffffff ? 0 : idx;
+    const float qscale = __uint_as_float(0x3DB504F3u);            // spec/layers.rs:146
+    for (int part = 0; part < 2; part++) {
+        const float inv = 1.0f / __builtin_sqrtf(block_treesum<true>(x + part * dk, dk, s, t) + eps);
+        float* dst = (part == 0 ? qb : kb) + (size_t)kh * dk;
+        for (int i = threadIdx.x; i < dk; i += RT) dst[i] = part == 0 ? (x[i] * inv) * qscale : x[dk + i] * inv;
+    }
+    for (int i = threadIdx.x; i < rep; i += RT) {
+        const int hv = kh * rep + i;
+        bd[2 * hv] = sigmoid_f(b[hv]);
+        bd[2 * hv + 1] = exp_f(-(A[hv] * softplus_f(a[hv] + dt_bias[hv])));
     }
 }
+
+// ------------------------------------------------------------------ argmax (spec/sample.rs:6-14)
+// The spec scans i = 1 .. V-1 and moves to i when l[i] > l[best]: the result is 0 when l[0] is NaN, else the lowest
+// index of the largest non-NaN value, with -0 equal to +0.  That is the maximum of the 64-bit keys
+// (order image of l[i] with -0 read as +0) << 32 | ~i, NaN keyed 0, so the rows' slices reduce in any order:
+// k_argmax_part takes the max over a slice of AMX_SLICE values and merges it into acc[row] by atomicMax;
+// k_argmax_fin decodes the key and leaves acc[row] at 0 for the next call.
+constexpr int AMX_SLICE = 2048;
+__device__ __forceinline__ unsigned long long amx_key(float v, int i) {
+    if (__builtin_isnan(v)) return 0ull;
+    const unsigned u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const unsigned o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)o << 32) | (unsigned long long)(~(unsigned)i);
+}
+__global__ void __launch_bounds__(RT) k_argmax_part(const float* __restrict__ logits, int V,
+                                                    unsigned long long* __restrict__ acc) {
+    __shared__ unsigned long long red[RT / 64];
+    const float* l = logits + (size_t)blockIdx.y * V;
+    const int i0 = blockIdx.x * AMX_SLICE + threadIdx.x;
+    constexpr int PER = AMX_SLICE / RT;
+    float v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) v[u] = i0 + u * RT < V ? l[i0 + u * RT] : __builtin_nanf("");
+    unsigned long long k = 0;
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const unsigned long long c = amx_key(v[u], i0 + u * RT);
+        k = c > k ? c : k;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long c = __shfl_xor(k, off, 64);
+        k = c > k ? c : k;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < RT / 64; w++) k = red[w] > k ? red[w] : k;
+        if (k) atomicMax(acc + blockIdx.y, k);
+    }
+}
+__global__ void k_argmax_fin(const float* __restrict__ logits, int M, int V, unsigned long long* __restrict__ acc,
+                             int* __restrict__ out) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= M) return;
+    const unsigned long long k = acc[row];
+    acc[row] = 0ull;
+    out[row] = (__builtin_isnan(logits[(size_t)row * V]) || k == 0ull) ? 0 : (int)~(unsigned)(k & 0xffffffffull);
+}
+
+// row accumulators of the argmax, zero between calls; library-owned, grown on demand
+unsigned long long* g_amx = nullptr;
+size_t g_amx_cap = 0;
 
 size_t gdn_scratch_floats(int M, int n_k, int n_v, int dk, int dv) {
     const size_t cd = 2 * (size_t)n_k * dk + (size_t)n_v * dv;
@@ -576,14 +650,23 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
     float* kb = qb + (size_t)M * n_k * dk;
     float* bd = kb + (size_t)M * n_k * dk;
     float* ob = bd + 2 * (size_t)M * n_v;
-    k_gdn_conv<<<dim3(M, (cd + RT - 1) / RT), RT, 0, st>>>(L->conv, S->conv_state, qkv, cd, y);
-    DET_CHECK(hipGetLastError());
-    k_gdn_conv_state<<<(cd + RT - 1) / RT, RT, 0, st>>>(S->conv_state, qkv, M, cd);
-    DET_CHECK(hipGetLastError());
-    int p = 1;
-    while (p < dk) p <<= 1;
-    k_gdn_prep<<<M * n_k, RT, ((size_t)dk + p + p / 2) * 4, st>>>(y, L->A, L->dt_bias, a, b, eps, n_k, n_v, dk, cd, qb, kb, bd);
-    DET_CHECK(hipGetLastError());
+    if (M == 1) {
+        // one decode token: conv, window update and prep in one launch
+        int p = 1;
+        while (p < dk) p <<= 1;
+        k_gdn_in1<<<n_k, RT, ((size_t)2 * dk + p + p / 2) * 4, st>>>(L->conv, S->conv_state, qkv, L->A, L->dt_bias, a, b,
+                                                                    eps, n_k, n_v, dk, dv, cd, y, qb, kb, bd);
+        DET_CHECK(hipGetLastError());
+    } else {
+        k_gdn_conv<<<dim3(M, (cd + RT - 1) / RT), RT, 0, st>>>(L->conv, S->conv_state, qkv, cd, y);
+        DET_CHECK(hipGetLastError());
+        k_gdn_conv_state<<<(cd + RT - 1) / RT, RT, 0, st>>>(S->conv_state, qkv, M, cd);
+        DET_CHECK(hipGetLastError());
+        int p = 1;
+        while (p < dk) p <<= 1;
+        k_gdn_prep<<<M * n_k, RT, ((size_t)dk + p + p / 2) * 4, st>>>(y, L->A, L->dt_bias, a, b, eps, n_k, n_v, dk, cd, qb, kb, bd);
+        DET_CHECK(hipGetLastError());
+    }
     // lanes per column: 16 (dk when dk < 16); blocks of GT / R columns, one workgroup each (grid y)
     const int R = dk < 16 ? dk : 16, CW = GT / R;
     const dim3 grid(n_v, (dv + CW - 1) / CW);
@@ -613,7 +696,18 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
 void det_argmax(const float* logits, int M, int V, int* out, hipStream_t st) {
     if (M < 1) return;
     if (V < 1) DET_FAIL("det_argmax: V=%d", V);
-    k_argmax<<<M, 1024, 0, st>>>(logits, V, out);
+    if (M > 65535) DET_FAIL("det_argmax: M=%d exceeds the grid", M);
+    if ((size_t)M > g_amx_cap) {
+        DET_CHECK(hipStreamSynchronize(st));     // earlier launches may still use the old buffer
+        if (g_amx) DET_CHECK(hipFree(g_amx));
+        g_amx_cap = std::max<size_t>(M, 256);
+        DET_CHECK(hipMalloc(&g_amx, g_amx_cap * 8));
+        DET_CHECK(hipMemset(g_amx, 0, g_amx_cap * 8));
+        DET_CHECK(hipDeviceSynchronize());
+    }
+    k_argmax_part<<<dim3((V + AMX_SLICE - 1) / AMX_SLICE, M), RT, 0, st>>>(logits, V, g_amx);
+    DET_CHECK(hipGetLastError());
+    k_argmax_fin<<<(M + 255) / 256, 256, 0, st>>>(logits, M, V, g_amx, out);
     DET_CHECK(hipGetLastError());
 }
 

@@ -136,3 +136,16 @@ def test_argmax_first_of_ties(V):
     L = oracle.lib()
     want = [L.ora_argmax(P(np.ascontiguousarray(x[m])), V) for m in range(3)]
     assert out.download().tolist() == want
+
+
+def test_argmax_nan_and_signed_zero():
+    """The spec's scan (l[i] > l[best]): a NaN at index 0 is kept, later NaNs are passed over, -0 equals +0."""
+    rows = [[np.nan, 1.0, 2.0, 0.5], [-0.0, 0.0, -1.0, -0.0], [1.0, np.nan, 3.0, 3.0], [-np.inf, np.nan, -np.inf, -np.inf],
+            [0.0, -0.0, np.nan, 0.0]]
+    x = np.array(rows, dtype=f32)
+    out = ffi.Buf(len(rows), np.int32)
+    ffi.argmax(ffi.Buf.upload(x), len(rows), 4, out)
+    L = oracle.lib()
+    want = [L.ora_argmax(P(np.ascontiguousarray(r)), 4) for r in x]
+    assert want == [0, 0, 2, 0, 0]
+    assert out.download().tolist() == want
