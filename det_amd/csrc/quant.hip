@@ -168,6 +168,126 @@ __global__ void __launch_bounds__(QT) k_quant(const float* __restrict__ a, const
     }
 }
 
+// Group mode with every thread holding EPT consecutive values of the row in registers (threads = n / EPT <= 1024,
+// one row per workgroup): the producer op, the RMSNorm sum, the group maxima (LPG = 128 / EPT lanes per group, DPP)
+// and the quantization run on registers, with two barriers in all (the standalone k_quant stages the row in LDS and
+// walks the groups wave by wave).  The operations are k_quant's: the RMSNorm sum is the spec's tree (a thread's
+// EPT leaves are an aligned subtree, then lane pairs by DPP and shuffles, then the waves' subtrees in order on 16
+// lanes, zero leaves past the row adding +0 to squares), the maxima are order-free.
+template <int LPG>
+__device__ __forceinline__ float group_max(float v) {
+    if (LPG >= 2) v = fmax_spec(v, dpp_f<0xB1>(v));
+    if (LPG >= 4) v = fmax_spec(v, dpp_f<0x4E>(v));
+    if (LPG >= 8) v = fmax_spec(v, dpp_f<0x141>(v));
+    if (LPG >= 16) v = fmax_spec(v, dpp_f<0x140>(v));
+    return v;
+}
+template <int MODE, int EPT>
+__global__ void __launch_bounds__(1024) k_qrow(const float* __restrict__ a, const float* __restrict__ b, float eps, int n,
+                                               float* __restrict__ y, int8_t* __restrict__ xq, float* __restrict__ sx,
+                                               uint16_t* __restrict__ mx) {
+    constexpr int LPG = GROUP / EPT;
+    __shared__ float red[16];
+    __shared__ float sg[1024];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, G = n / GROUP;
+    const int i0 = tid * EPT;
+    const bool live = i0 < n;                          // n is a multiple of 128, so a thread is all in or all out
+    const size_t off = (size_t)row * n + i0;
+    float v[EPT], u[EPT];
+    if (live) {
+#pragma unroll
+        for (int k = 0; k < EPT; k += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(a + off + k);
+            v[k] = t.x; v[k + 1] = t.y; v[k + 2] = t.z; v[k + 3] = t.w;
+            if (MODE != MODE_QUANT) {
+                const float4 q = *reinterpret_cast<const float4*>(b + (MODE == MODE_RMSNORM ? (size_t)i0 : off) + k);
+                u[k] = q.x; u[k + 1] = q.y; u[k + 2] = q.z; u[k + 3] = q.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < EPT; k++) { v[k] = 0.0f; u[k] = 0.0f; }
+    }
+    if (MODE == MODE_SILU_MUL) {
+#pragma unroll
+        for (int k = 0; k < EPT; k++) v[k] = silu_f(v[k]) * u[k];
+    }
+    if (MODE == MODE_RMSNORM) {
+        float sq[EPT];
+#pragma unroll
+        for (int k = 0; k < EPT; k++) sq[k] = v[k] * v[k];
+        float ts = tree_reg<EPT>(sq);
+        ts = lane_tree_sum<16>(ts);
+        ts = ts + __shfl_xor(ts, 16, 64);
+        ts = ts + __shfl_xor(ts, 32, 64);
+        if (lane == 0) red[wv] = ts;
+        __syncthreads();
+        const int nw = (int)(blockDim.x >> 6);
+        float w = lane < nw && lane < 16 ? red[lane] : 0.0f;
+        w = lane_tree_sum<16>(w);
+        const float ss = __shfl(w, 0, 64);
+        const float inv = 1.0f / __builtin_sqrtf((ss / (float)n) + eps);
+#pragma unroll
+        for (int k = 0; k < EPT; k++) v[k] = (v[k] * inv) * u[k];
+    }
+    if (y && live) {
+#pragma unroll
+        for (int k = 0; k < EPT; k += 4) *reinterpret_cast<float4*>(y + off + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+    }
+    if (!xq) return;
+    // spec/quant.rs:21-49
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < EPT; k++) am = fmax_spec(am, __builtin_fabsf(v[k]));
+    am = group_max<LPG>(am);
+    const int g = tid / LPG;
+    if (live && tid % LPG == 0) sg[g] = am / 127.0f;
+    __syncthreads();
+    float smax = 0.0f;
+    for (int j = lane; j < G; j += 64) smax = fmax_spec(smax, sg[j]);
+    smax = wave_max(smax);
+    const float s = smax == 0.0f ? 1.0f : smax / 65535.0f;
+    if (!live) return;
+    float m = rint_(sg[g] / s);
+    if (m < 1.0f) m = 1.0f;
+    else if (m > 65535.0f) m = 65535.0f;
+    const unsigned int mi = __builtin_isnan(m) ? 0u : (unsigned int)m;
+    const float inv = 1.0f / (s * (float)mi);
+    uint32_t pk[EPT / 4];
+#pragma unroll
+    for (int k = 0; k < EPT; k += 4) {
+        uint32_t wd = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) wd |= ((uint32_t)(uint8_t)(int8_t)clamp_i8(rint_(v[k + j] * inv))) << (8 * j);
+        pk[k / 4] = wd;
+    }
+    uint32_t* qd = reinterpret_cast<uint32_t*>(xq + off);
+#pragma unroll
+    for (int k = 0; k < EPT / 4; k++) qd[k] = pk[k];
+    if (tid % LPG == 0) mx[(size_t)row * G + g] = (uint16_t)mi;
+    if (tid == 0) sx[row] = s;
+}
+
+// k_qrow when it applies: group mode, 16-byte aligned rows, n / EPT <= 1024 threads (EPT = 8 up to n = 8192, 16 up
+// to 16384, 32 up to 32768).  Returns false to leave the call to k_quant.
+template <int MODE>
+bool launch_qrow(const float* a, const float* b, float eps, int M, int n, float* y, int8_t* xq, float* sx, uint16_t* mx,
+                 hipStream_t st) {
+    if (!mx || !xq || n % GROUP) return false;
+    const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al(a) || (b && !al(b)) || (y && !al(y)) || !al(xq)) return false;
+    const int ept = n <= 8192 ? 8 : n <= 16384 ? 16 : n <= 32768 ? 32 : 0;
+    if (!ept) return false;
+    const int threads = ((n / ept + 63) / 64) * 64;
+    switch (ept) {
+    case 8: k_qrow<MODE, 8><<<M, threads, 0, st>>>(a, b, eps, n, y, xq, sx, mx); break;
+    case 16: k_qrow<MODE, 16><<<M, threads, 0, st>>>(a, b, eps, n, y, xq, sx, mx); break;
+    default: k_qrow<MODE, 32><<<M, threads, 0, st>>>(a, b, eps, n, y, xq, sx, mx); break;
+    }
+    DET_CHECK(hipGetLastError());
+    return true;
+}
+
 template <int MODE>
 void launch(const float* a, const float* b, float eps, int M, int n, float* y, int8_t* xq, float* sx, uint16_t* mx,
             hipStream_t st, const char* who) {
@@ -180,6 +300,7 @@ void launch(const float* a, const float* b, float eps, int M, int n, float* y, i
     if (MODE == MODE_RMSNORM && p > 8192) DET_FAIL("%s: unsupported n=%d", who, n);
     const size_t lds = (size_t)n * 4;
     if (lds > 150 * 1024) DET_FAIL("%s: row of n=%d does not fit in LDS", who, n);
+    if (launch_qrow<MODE>(a, b, eps, M, n, y, xq, sx, mx, st)) return;
     static bool attr = false;
     if (!attr) {
         DET_CHECK(hipFuncSetAttribute((const void*)k_quant<MODE, QT_MANY>, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024));
