@@ -85,7 +85,7 @@ __device__ float block_quant_i8(const float* x, int n, int8_t* q, float* red) {
 // ------------------------------------------------------------------ attention (cpu.rs:212-285)
 // One workgroup per (token, kv head): k -> rmsnorm(k_norm) -> rope -> quant_act_i8 into kq / sk at row pos0 + t,
 // v -> quant_v (spec/layers.rs:73-86) into vq.  LDS: x[hd], tree s[p], t[p / 2].
-__global__ void __launch_bounds__(RT) k_attn_kv(const float* __restrict__ k_norm, const float* __restrict__ v_inv_scale,
+__device__ __forceinline__ void attn_kv_row(int kvrow, const float* __restrict__ k_norm, const float* __restrict__ v_inv_scale,
                                                 int8_t* __restrict__ kq, float* __restrict__ sk, int16_t* __restrict__ vq,
                                                 const float* __restrict__ k, const float* __restrict__ v,
                                                 const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
@@ -95,7 +95,7 @@ __global__ void __launch_bounds__(RT) k_attn_kv(const float* __restrict__ k_norm
     float* x = lds;
     float* s = x + hd;
     float* t = s + p2(hd);
-    const int tok = blockIdx.x / n_kv, h = blockIdx.x - tok * n_kv, pos = pos0 + tok;
+    const int tok = kvrow / n_kv, h = kvrow - tok * n_kv, pos = pos0 + tok;
     const size_t src = ((size_t)tok * n_kv + h) * hd;
     for (int i = threadIdx.x; i < hd; i += RT) x[i] = k[src + i];
     __syncthreads();
@@ -116,12 +116,13 @@ __global__ void __launch_bounds__(RT) k_attn_kv(const float* __restrict__ k_norm
 // integer, den = sum pq_j, num_i = sum pq_j vq_j[i], o_i = ((f32(num_i) / f32(den)) * v_scale) * sigmoid(gate_i).
 // The max is order-free and the sums are exact integers, so the keys are split into chunks of CK, one workgroup
 // each (grid x = chunk, grid y = token * n_h + head), and the chunks meet through device atomics:
-//   k_attn_q   q -> rmsnorm(q_norm) -> rope -> * 1/sqrt(hd) -> quant_act_i8 into scratch; clears the head's
-//              max, den and num (so no memset is needed and the launches can be captured);
-//   k_attn_max the chunk's scores and their max, merged by atomicMax on an order-preserving integer image;
-//   k_attn_acc the chunk's scores again (same integers, same fp32 ops), its pq_j, and the chunk's den and num
-//              partials added by int64 atomics;
-//   k_attn_fin the output.
+//   k_attn_prep the cache rows of the new k and v (k_attn_kv's work) and the q rows: q -> rmsnorm(q_norm) -> rope
+//              -> * 1/sqrt(hd) -> quant_act_i8 into scratch, clearing the head's max, den, num and chunk counter
+//              (so no memset is needed and the launches can be captured);
+//   k_attn_max  the chunk's scores and their max, merged by atomicMax on an order-preserving integer image;
+//   k_attn_acc  the chunk's scores again (same integers, same fp32 ops), its pq_j, and the chunk's den and num
+//              partials added by int64 atomics; for a few tokens the row's last chunk to count itself writes the
+//              output, for a batch k_attn_fin does (waiting for the atomics in every workgroup costs more there).
 // A score takes 16 lanes: lane l reads words l, l + 16, ... of the key row (coalesced) into v_dot4 sums, and the
 // 16 partial sums meet by DPP exchanges (integers: any order).
 struct AttnScratch {
@@ -130,6 +131,7 @@ struct AttnScratch {
     unsigned* mxo;    // [M][n_h] order-preserving image of the max
     long long* den;   // [M][n_h]
     long long* num;   // [M][n_h][hd]
+    unsigned* cnt;    // [M][n_h] chunks of the row that have added their sums
     size_t bytes;
 };
 __host__ __device__ inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -143,6 +145,7 @@ inline AttnScratch attn_layout(void* base, int M, int n_h, int hd) {
     S.mxo = reinterpret_cast<unsigned*>(p + off);  off += al256(r * 4);
     S.den = reinterpret_cast<long long*>(p + off); off += al256(r * 8);
     S.num = reinterpret_cast<long long*>(p + off); off += al256(r * hd * 8);
+    S.cnt = reinterpret_cast<unsigned*>(p + off);  off += al256(r * 4);
     S.bytes = off;
     return S;
 }
@@ -167,7 +170,7 @@ __device__ __forceinline__ int sum16(int v) {       // every lane of an aligned 
 }
 constexpr int AQW = 16;     // max words (4 codes each) per lane of a score: hd <= 1024
 
-__global__ void __launch_bounds__(RT) k_attn_q(const float* __restrict__ q_norm, const float* __restrict__ qg,
+__device__ __forceinline__ void attn_q_row(int qrow, const float* __restrict__ q_norm, const float* __restrict__ qg,
                                                const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
                                                int half, float eps, int pos0, int n_h, int hd, AttnScratch S) {
     extern __shared__ float lds[];
@@ -176,7 +179,7 @@ __global__ void __launch_bounds__(RT) k_attn_q(const float* __restrict__ q_norm,
     float* x = lds;
     float* s = x + hd;
     float* t = s + p;
-    const int row = blockIdx.x, tok = row / n_h, pos = pos0 + tok;
+    const int row = qrow, tok = row / n_h, pos = pos0 + tok;
     const float* qr = qg + (size_t)row * 2 * hd;
     for (int i = threadIdx.x; i < hd; i += RT) x[i] = qr[i];
     __syncthreads();
@@ -191,7 +194,21 @@ __global__ void __launch_bounds__(RT) k_attn_q(const float* __restrict__ q_norm,
         S.sq[row] = sq;
         S.mxo[row] = 0u;
         S.den[row] = 0;
+        S.cnt[row] = 0u;
     }
+}
+
+// the k rows, v rows and q rows of the call in one launch: workgroups 0 .. nkv - 1 take (token, kv head) rows,
+// the rest (token, head) rows
+__global__ void __launch_bounds__(RT) k_attn_prep(const float* __restrict__ k_norm, const float* __restrict__ v_inv_scale,
+                                                  int8_t* __restrict__ kq, float* __restrict__ sk, int16_t* __restrict__ vq,
+                                                  const float* __restrict__ k, const float* __restrict__ v,
+                                                  const float* __restrict__ q_norm, const float* __restrict__ qg,
+                                                  const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+                                                  int half, float eps, int pos0, int n_kv, int n_h, int hd, int nkv,
+                                                  AttnScratch S) {
+    if ((int)blockIdx.x < nkv) attn_kv_row(blockIdx.x, k_norm, v_inv_scale, kq, sk, vq, k, v, rope_cos, rope_sin, half, eps, pos0, n_kv, hd);
+    else attn_q_row(blockIdx.x - nkv, q_norm, qg, rope_cos, rope_sin, half, eps, pos0, n_h, hd, S);
 }
 
 // scores of the chunk's keys for this thread's 16-lane row: calls f(key, score) on lane 0 of the row for every key
@@ -237,12 +254,14 @@ __global__ void __launch_bounds__(RT) k_attn_max(const int8_t* __restrict__ kq, 
     }
 }
 
-template <int CK>
+template <int CK, bool FIN>
 __global__ void __launch_bounds__(RT) k_attn_acc(const int8_t* __restrict__ kq, const float* __restrict__ sk,
                                                  const int16_t* __restrict__ vq, int pos0, int n_h, int n_kv, int hd,
-                                                 AttnScratch S) {
+                                                 AttnScratch S, const float* __restrict__ v_scale,
+                                                 const float* __restrict__ qg, float* __restrict__ o) {
     __shared__ int pqs[CK];
     __shared__ long long dens[RT / 64];
+    __shared__ unsigned last;
     const int row = blockIdx.y, tok = row / n_h, h = row - tok * n_h, kvh = h / (n_h / n_kv);
     const int nkeys = pos0 + tok + 1, j0 = blockIdx.x * CK;
     if (j0 >= nkeys) return;
@@ -271,8 +290,25 @@ __global__ void __launch_bounds__(RT) k_attn_acc(const int8_t* __restrict__ kq, 
         for (int jj = 0; jj < nc; jj++) acc += (long long)pqs[jj] * (long long)vb[jj * vstride + i];
         atomicAdd(reinterpret_cast<unsigned long long*>(S.num + (size_t)row * hd + i), (unsigned long long)acc);
     }
+    if (!FIN) return;
+    // the row's last chunk to arrive writes the output (its sums are complete once every chunk's adds are performed)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(S.cnt + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)((nkeys + CK - 1) / CK - 1);
+    __syncthreads();
+    if (!last) return;
+    const float fden = i64_to_f(__hip_atomic_load(S.den + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const float vs = v_scale[kvh];
+    const float* gate = qg + (size_t)row * 2 * hd + hd;
+    for (int i = threadIdx.x; i < hd; i += RT) {
+        const long long nm = __hip_atomic_load(S.num + (size_t)row * hd + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        o[(size_t)row * hd + i] = ((i64_to_f(nm) / fden) * vs) * sigmoid_f(gate[i]);
+    }
 }
 
+
+// the output of a batch's rows once every chunk has added its sums (k_attn_acc<CK, false>)
 __global__ void __launch_bounds__(RT) k_attn_fin(const float* __restrict__ v_scale, const float* __restrict__ qg,
                                                  int n_h, int n_kv, int hd, AttnScratch S, float* __restrict__ o) {
     const int row = blockIdx.x, h = row % n_h, kvh = h / (n_h / n_kv);
@@ -372,8 +408,11 @@ template <int RB, int R>
 __global__ void __launch_bounds__(GT) k_gdn_rec(float* __restrict__ S, const float* __restrict__ qb,
                                                 const float* __restrict__ kb, const float* __restrict__ y,
                                                 const float* __restrict__ bd, int M, int n_k, int n_v, int dv, int cd,
-                                                float* __restrict__ ob) {
+                                                float* __restrict__ ob, const float* __restrict__ norm,
+                                                const float* __restrict__ z, float eps, float* __restrict__ on,
+                                                unsigned* __restrict__ cnt) {
     constexpr int DK = R * RB, TC = GTC, CW = GT / R;
+    __shared__ unsigned last;
     constexpr int LK = (TC * DK + GT - 1) / GT, LV = (TC * CW + GT - 1) / GT;
     constexpr int BUF = 2 * TC * DK + TC * CW + 2 * TC;           // floats of one buffer: k, q, v, (beta, decay)
     extern __shared__ float sm[];
@@ -451,7 +490,11 @@ __global__ void __launch_bounds__(GT) k_gdn_rec(float* __restrict__ S, const flo
 #pragma unroll
             for (int i = 0; i < RB; i++) p[i] = col[i] * qc[i];
             const float oj = lane_tree_sum<R>(reg_tree<RB>(p));
-            if (live && r == 0) ob[((size_t)(c0 + tt) * n_v + h) * dv + j] = oj;
+            if (live && r == 0) {
+                float* dst = ob + ((size_t)(c0 + tt) * n_v + h) * dv + j;
+                if (cnt) __hip_atomic_store(dst, oj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else *dst = oj;
+            }
 #pragma unroll
             for (int i = 0; i < RB; i++) { kc[i] = kn[i]; qc[i] = qn[i]; }
             beta = bn;
@@ -466,6 +509,21 @@ __global__ void __launch_bounds__(GT) k_gdn_rec(float* __restrict__ S, const flo
 #pragma unroll
         for (int i = 0; i < RB; i++) Sh[(size_t)(r * RB + i) * dv + j] = col[i];
     }
+    if (!cnt) return;
+    // one token (cnt != NULL): the head's last column block to count itself runs the gated norm (k_gdn_out) on the
+    // head's output, which every block stored with agent-scope stores that have been performed
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) last = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+    __syncthreads();
+    if (!last) return;
+    float* x = sm;
+    float* s2 = x + dv;
+    float* t2 = s2 + p2(dv);
+    for (int i = tid; i < dv; i += GT) x[i] = __hip_atomic_load(ob + (size_t)h * dv + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    block_rmsnorm(x, dv, norm, eps, s2, t2);
+    for (int i = tid; i < dv; i += GT) on[(size_t)h * dv + i] = x[i] * silu_f(z[(size_t)h * dv + i]);
 }
 
 // gated norm: on = rmsnorm(o, norm) * silu(z) per (token, v head)
@@ -492,7 +550,7 @@ __global__ void __launch_bounds__(RT) k_gdn_in1(const float* __restrict__ conv_w
                                                 const float* __restrict__ dt_bias, const float* __restrict__ a,
                                                 const float* __restrict__ b, float eps, int n_k, int n_v, int dk, int dv,
                                                 int cd, float* __restrict__ y, float* __restrict__ qb,
-                                                float* __restrict__ kb, float* __restrict__ bd) {
+                                                float* __restrict__ kb, float* __restrict__ bd, unsigned* __restrict__ cnt) {
     extern __shared__ float lds[];
     const int p = p2(dk);
     float* x = lds;                  // conv q [dk], then conv k [dk]
@@ -525,6 +583,7 @@ __global__ void __launch_bounds__(RT) k_gdn_in1(const float* __restrict__ conv_w
     }
     for (int i = threadIdx.x; i < rep; i += RT) {
         const int hv = kh * rep + i;
+        cnt[hv] = 0u;                                 // the fused gated norm's arrival counter of v head hv
         bd[2 * hv] = sigmoid_f(b[hv]);
         bd[2 * hv + 1] = exp_f(-(A[hv] * softplus_f(a[hv] + dt_bias[hv])));
     }
@@ -585,7 +644,7 @@ size_t g_amx_cap = 0;
 
 size_t gdn_scratch_floats(int M, int n_k, int n_v, int dk, int dv) {
     const size_t cd = 2 * (size_t)n_k * dk + (size_t)n_v * dv;
-    return (size_t)M * cd + 2 * (size_t)M * n_k * dk + 2 * (size_t)M * n_v + (size_t)M * n_v * dv;
+    return (size_t)M * cd + 2 * (size_t)M * n_k * dk + 2 * (size_t)M * n_v + (size_t)M * n_v * dv + (size_t)n_v;
 }
 
 } // namespace
@@ -609,11 +668,9 @@ void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float*
     int p = 1;
     while (p < hd) p <<= 1;
     const size_t lds_row = ((size_t)hd + p + p / 2) * 4;
-    k_attn_kv<<<M * n_kv, RT, lds_row, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, rope_cos, rope_sin,
-                                             rot / 2, eps, pos0, n_kv, hd);
-    DET_CHECK(hipGetLastError());
     const AttnScratch S = attn_layout(scratch, M, n_h, hd);
-    k_attn_q<<<M * n_h, RT, lds_row, st>>>(L->q_norm, qg, rope_cos, rope_sin, rot / 2, eps, pos0, n_h, hd, S);
+    k_attn_prep<<<M * (n_kv + n_h), RT, lds_row, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, L->q_norm, qg,
+                                                      rope_cos, rope_sin, rot / 2, eps, pos0, n_kv, n_h, hd, M * n_kv, S);
     DET_CHECK(hipGetLastError());
     // chunks of 32 keys for a few tokens (a decode step: many workgroups per head), 256 for a batch
     const int nkeys = pos0 + M;
@@ -621,15 +678,15 @@ void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float*
         const dim3 grid((nkeys + 31) / 32, M * n_h);
         k_attn_max<32><<<grid, RT, 0, st>>>(kv->kq, kv->sk, pos0, n_h, n_kv, hd, S);
         DET_CHECK(hipGetLastError());
-        k_attn_acc<32><<<grid, RT, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, n_h, n_kv, hd, S);
+        k_attn_acc<32, true><<<grid, RT, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, n_h, n_kv, hd, S, L->v_scale, qg, o);
     } else {
         const dim3 grid((nkeys + 255) / 256, M * n_h);
         k_attn_max<256><<<grid, RT, 0, st>>>(kv->kq, kv->sk, pos0, n_h, n_kv, hd, S);
         DET_CHECK(hipGetLastError());
-        k_attn_acc<256><<<grid, RT, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, n_h, n_kv, hd, S);
+        k_attn_acc<256, false><<<grid, RT, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, n_h, n_kv, hd, S, L->v_scale, qg, o);
+        DET_CHECK(hipGetLastError());
+        k_attn_fin<<<M * n_h, RT, 0, st>>>(L->v_scale, qg, n_h, n_kv, hd, S, o);
     }
-    DET_CHECK(hipGetLastError());
-    k_attn_fin<<<M * n_h, RT, 0, st>>>(L->v_scale, qg, n_h, n_kv, hd, S, o);
     DET_CHECK(hipGetLastError());
 }
 
@@ -650,12 +707,13 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
     float* kb = qb + (size_t)M * n_k * dk;
     float* bd = kb + (size_t)M * n_k * dk;
     float* ob = bd + 2 * (size_t)M * n_v;
+    unsigned* cnt = M == 1 ? reinterpret_cast<unsigned*>(ob + (size_t)M * n_v * dv) : nullptr;   // [n_v]
     if (M == 1) {
         // one decode token: conv, window update and prep in one launch
         int p = 1;
         while (p < dk) p <<= 1;
         k_gdn_in1<<<n_k, RT, ((size_t)2 * dk + p + p / 2) * 4, st>>>(L->conv, S->conv_state, qkv, L->A, L->dt_bias, a, b,
-                                                                    eps, n_k, n_v, dk, dv, cd, y, qb, kb, bd);
+                                                                    eps, n_k, n_v, dk, dv, cd, y, qb, kb, bd, cnt);
         DET_CHECK(hipGetLastError());
     } else {
         k_gdn_conv<<<dim3(M, (cd + RT - 1) / RT), RT, 0, st>>>(L->conv, S->conv_state, qkv, cd, y);
@@ -679,14 +737,15 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
         attr = true;
     }
     switch (dk) {
-    case 4: k_gdn_rec<1, 4><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 8: k_gdn_rec<1, 8><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 16: k_gdn_rec<1, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 32: k_gdn_rec<2, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    case 64: k_gdn_rec<4, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
-    default: k_gdn_rec<8, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob); break;
+    case 4: k_gdn_rec<1, 4><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob, L->norm, z, eps, on, cnt); break;
+    case 8: k_gdn_rec<1, 8><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob, L->norm, z, eps, on, cnt); break;
+    case 16: k_gdn_rec<1, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob, L->norm, z, eps, on, cnt); break;
+    case 32: k_gdn_rec<2, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob, L->norm, z, eps, on, cnt); break;
+    case 64: k_gdn_rec<4, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob, L->norm, z, eps, on, cnt); break;
+    default: k_gdn_rec<8, 16><<<grid, GT, rl, st>>>(S->S, qb, kb, y, bd, M, n_k, n_v, dv, cd, ob, L->norm, z, eps, on, cnt); break;
     }
     DET_CHECK(hipGetLastError());
+    if (cnt) return;                                  // one token: the recurrence's last block of each head ran the gated norm
     int pv = 1;
     while (pv < dv) pv <<= 1;
     k_gdn_out<<<M * n_v, RT, ((size_t)dv + pv + pv / 2) * 4, st>>>(ob, L->norm, z, eps, dv, on);
