@@ -63,6 +63,13 @@ __host__ __device__ __forceinline__ float i64_to_f(long long v) {
     return v < 0 ? -f : f;
 }
 
+// int64 += int32 * uint32 (one 32x32->64 unsigned multiply-add and a sign fix of the high word)
+__device__ __forceinline__ void mac_s32_u32(long long& acc, int p, uint32_t s) {
+    unsigned long long r = (unsigned long long)(uint32_t)p * (unsigned long long)s + (unsigned long long)acc;
+    r -= (unsigned long long)(s & (uint32_t)(p >> 31)) << 32;
+    acc = (long long)r;
+}
+
 // ---- spec/prim.rs:78-149 transcendental op sequences (Cephes-derived, explicit fp32 ops; no libm).
 // Constants are binary64 literals rounded once to binary32, as spec/prim.rs:4-35 writes them.
 __device__ __forceinline__ float exp_f(float x) {

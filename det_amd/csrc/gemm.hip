@@ -118,13 +118,6 @@ template <> __device__ __forceinline__ void block_unsigned<8>(const uint32_t* q,
     for (int j = 0; j < 8; j++) u[j] = q[j];
 }
 
-// int64 += int32 * uint32 (one 32x32->64 unsigned multiply-add and a sign fix of the high word)
-__device__ __forceinline__ void mac_s32_u32(long long& acc, int p, uint32_t s) {
-    unsigned long long r = (unsigned long long)(uint32_t)p * (unsigned long long)s + (unsigned long long)acc;
-    r -= (unsigned long long)(s & (uint32_t)(p >> 31)) << 32;
-    acc = (long long)r;
-}
-
 // ------------------------------------------------------------------ global -> LDS copies
 // Global -> LDS copy by the buffer unit (BYTES = 4 or 16 per lane, lane i's bytes land at lds + i * BYTES), written as
 // inline assembly so that the compiler does not track it: with the builtin it cannot tell that later LDS reads touch

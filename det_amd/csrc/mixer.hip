@@ -9,6 +9,7 @@
 // int64 integers (order-free).
 #include <algorithm>
 #include "common.h"
+#include "mixer_internal.h"
 #include "../../include/det_hip.h"
 using namespace det;
 
@@ -550,7 +551,9 @@ __global__ void __launch_bounds__(RT) k_gdn_in1(const float* __restrict__ conv_w
                                                 const float* __restrict__ dt_bias, const float* __restrict__ a,
                                                 const float* __restrict__ b, float eps, int n_k, int n_v, int dk, int dv,
                                                 int cd, float* __restrict__ y, float* __restrict__ qb,
-                                                float* __restrict__ kb, float* __restrict__ bd, unsigned* __restrict__ cnt) {
+                                                float* __restrict__ kb, float* __restrict__ bd, unsigned* __restrict__ cnt,
+                                                det_qlinear ab, const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                const uint16_t* __restrict__ mx) {
     extern __shared__ float lds[];
     const int p = p2(dk);
     float* x = lds;                  // conv q [dk], then conv k [dk]
@@ -581,11 +584,38 @@ __global__ void __launch_bounds__(RT) k_gdn_in1(const float* __restrict__ conv_w
         float* dst = (part == 0 ? qb : kb) + (size_t)kh * dk;
         for (int i = threadIdx.x; i < dk; i += RT) dst[i] = part == 0 ? (x[i] * inv) * qscale : x[dk + i] * inv;
     }
+    __shared__ float abv[2 * 64];
+    if (ab.wq) {
+        // the a|b projection of the token (a W8 linear of 2 n_v rows: a heads, then b heads), the same integers and
+        // epilogue as det_gemm_ex: wave w takes the rows w, w + 4, ... of this k head's 2 rep; lane l the 16-code
+        // chunks l, l + 64, ... of the row; each chunk's v_dot4 sum is scaled by its group's m * mx into int64
+        const int G = ab.K / GROUP, lane = threadIdx.x & 63;
+        for (int e = threadIdx.x >> 6; e < 2 * rep; e += RT / 64) {
+            const int R = e < rep ? kh * rep + e : n_v + kh * rep + (e - rep), tile = R / 64, rr = R % 64;
+            long long acc = 0;
+            for (int ch = lane; ch < G * 8; ch += 64) {
+                const int g = ch >> 3;
+                const size_t tg = (size_t)tile * G + g;
+                const int4 w4 = *reinterpret_cast<const int4*>(ab.wq + ((tg * 8 + (ch & 7)) * 64 + rr) * 16);
+                const int4 x4 = *reinterpret_cast<const int4*>(xq + (size_t)ch * 16);
+                int p = __builtin_amdgcn_sdot4(w4.x, x4.x, 0, false);
+                p = __builtin_amdgcn_sdot4(w4.y, x4.y, p, false);
+                p = __builtin_amdgcn_sdot4(w4.z, x4.z, p, false);
+                p = __builtin_amdgcn_sdot4(w4.w, x4.w, p, false);
+                mac_s32_u32(acc, p, (uint32_t)ab.m[tg * 64 + rr] * (mx ? (uint32_t)mx[g] : 1u));
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+            if (lane == 0) abv[e] = (i64_to_f(acc) * ab.c[R]) * sx[0];
+        }
+        __syncthreads();
+    }
     for (int i = threadIdx.x; i < rep; i += RT) {
         const int hv = kh * rep + i;
         cnt[hv] = 0u;                                 // the fused gated norm's arrival counter of v head hv
-        bd[2 * hv] = sigmoid_f(b[hv]);
-        bd[2 * hv + 1] = exp_f(-(A[hv] * softplus_f(a[hv] + dt_bias[hv])));
+        const float av = ab.wq ? abv[i] : a[hv], bv = ab.wq ? abv[rep + i] : b[hv];
+        bd[2 * hv] = sigmoid_f(bv);
+        bd[2 * hv + 1] = exp_f(-(A[hv] * softplus_f(av + dt_bias[hv])));
     }
 }
 
@@ -696,11 +726,23 @@ size_t det_gdn_scratch_bytes(int M, int n_k, int n_v, int dk, int dv) {
 
 void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const float* z, const float* a, const float* b,
              float eps, int M, int n_k, int n_v, int dk, int dv, float* on, void* scratch, hipStream_t st) {
+    det::gdn_run(L, S, qkv, z, a, b, nullptr, nullptr, nullptr, nullptr, eps, M, n_k, n_v, dk, dv, on, scratch, st);
+}
+
+} // extern "C"
+
+namespace det {
+
+void gdn_run(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const float* z, const float* a, const float* b,
+             const det_qlinear* ab, const int8_t* xq, const float* sx, const uint16_t* mx, float eps, int M, int n_k,
+             int n_v, int dk, int dv, float* on, void* scratch, hipStream_t st) {
     if (M < 1) return;
     if (n_k < 1 || n_v < n_k || n_v % n_k) DET_FAIL("det_gdn: %d v heads over %d k heads", n_v, n_k);
     if (dk < 4 || dk > 128 || (dk & (dk - 1))) DET_FAIL("det_gdn: dk %d (a power of two, 4 .. 128)", dk);
     if (dv < 1 || dv > 256) DET_FAIL("det_gdn: dv %d (at most 256)", dv);
     if (!scratch) DET_FAIL("det_gdn: scratch of det_gdn_scratch_bytes() is required");
+    if (ab && (M != 1 || ab->bits != 8 || ab->N != 2 * n_v || n_v / n_k > 64 || !xq || !sx))
+        DET_FAIL("det_gdn: the fused a|b projection needs one token, a W8 linear of 2 n_v rows and rep <= 64");
     const int cd = 2 * n_k * dk + n_v * dv;
     float* y = static_cast<float*>(scratch);
     float* qb = y + (size_t)M * cd;
@@ -713,7 +755,8 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
         int p = 1;
         while (p < dk) p <<= 1;
         k_gdn_in1<<<n_k, RT, ((size_t)2 * dk + p + p / 2) * 4, st>>>(L->conv, S->conv_state, qkv, L->A, L->dt_bias, a, b,
-                                                                    eps, n_k, n_v, dk, dv, cd, y, qb, kb, bd, cnt);
+                                                                    eps, n_k, n_v, dk, dv, cd, y, qb, kb, bd, cnt,
+                                                                    ab ? *ab : det_qlinear{}, xq, sx, mx);
         DET_CHECK(hipGetLastError());
     } else {
         k_gdn_conv<<<dim3(M, (cd + RT - 1) / RT), RT, 0, st>>>(L->conv, S->conv_state, qkv, cd, y);
@@ -751,6 +794,10 @@ void det_gdn(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
     k_gdn_out<<<M * n_v, RT, ((size_t)dv + pv + pv / 2) * 4, st>>>(ob, L->norm, z, eps, dv, on);
     DET_CHECK(hipGetLastError());
 }
+
+} // namespace det
+
+extern "C" {
 
 void det_argmax(const float* logits, int M, int V, int* out, hipStream_t st) {
     if (M < 1) return;

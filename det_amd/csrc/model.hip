@@ -6,6 +6,7 @@
 #include <vector>
 #include "common.h"
 #include "gguf_reader.h"
+#include "mixer_internal.h"
 #include "../../include/det_hip.h"
 #include "../../include/det_model.h"
 
@@ -324,8 +325,12 @@ void forward_layers(det_model* m, int pos0, int t) {
             det_gemm_ex(&L.a.o.lins[0].q, m->oq, m->so, m->mo, t, m->x, 1, 0, nullptr, nullptr, st);
         } else {
             m->project(L.g.qkvz, m->xq, m->sx, m->mx, t, {m->qkv, m->z});
-            m->project(L.g.ab, m->xq, m->sx, m->mx, t, {m->a, m->b});
-            det_gdn(&L.g.layer, &L.g.state, m->qkv, m->z, m->a, m->b, eps, t, n_k, n_v, dk, dv, m->on, m->gdn_scratch, st);
+            // one token with det's default W8 a|b: the projection runs inside the GDN input stage (one launch less)
+            const bool fuse_ab = t == 1 && L.g.ab.lins.size() == 1 && L.g.ab.lins[0].q.bits == 8 &&
+                                 L.g.ab.lins[0].q.N == 2 * n_v && n_v / n_k <= 64;
+            if (!fuse_ab) m->project(L.g.ab, m->xq, m->sx, m->mx, t, {m->a, m->b});
+            det::gdn_run(&L.g.layer, &L.g.state, m->qkv, m->z, m->a, m->b, fuse_ab ? &L.g.ab.lins[0].q : nullptr, m->xq,
+                         m->sx, m->mx, eps, t, n_k, n_v, dk, dv, m->on, m->gdn_scratch, st);
             det_quant(m->on, t, n_v * dv, m->onq, m->son, m->mon, st);
             det_gemm_ex(&L.g.out.lins[0].q, m->onq, m->son, m->mon, t, m->x, 1, 0, nullptr, nullptr, st);
         }
