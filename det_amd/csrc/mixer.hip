@@ -309,6 +309,201 @@ __global__ void __launch_bounds__(RT) k_attn_acc(const int8_t* __restrict__ kq, 
 }
 
 
+// ---- a batch on the matrix cores (k_attn_mma): the same integers and fp32 operations as k_attn_max / k_attn_acc.
+// Workgroup = (32 output dims, 16 tokens, up to 4 q heads of one kv head: a wave each); keys in chunks of 64 staged
+// in LDS and shared by the heads.  Scores: v_mfma_i32_16x16x64_i8 of the int8 q rows by the int8 key rows (exact
+// int32 dots), then (f32(dot) * sq) * sk.  Pass 1 folds the row maxima (order-free); pass 2 recomputes the scores,
+// forms pq = rint(exp(s - mx) * 2^24) and the exact products with the int16 values as digit products on the matrix
+// core: pq = sum_a 2^(7 a) p_a with unsigned 7-bit p_0..p_2 and p_3 <= 8, v = sum_b 2^(7 b) v_b with balanced
+// 7-bit v_0, v_1 in [-64, 63] and v_2 in [-2, 2], so num = sum_{a,b} 2^(7 (a + b)) (P_a V_b) with every P_a V_b an
+// exact int32 sum (|p_a v_b| <= 127 * 64, fewer than 2^18 keys).  P reaches the A-operand layout through a
+// wave-private LDS tile; V's digits are staged transposed ([dim][key]) so a lane's 16 keys are contiguous.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+constexpr int AM_T = 16, AM_KC = 64, AM_D = 32;
+template <int CTRL>
+__device__ __forceinline__ long long dpp_ll(long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(v & 0xffffffffll), CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, 0xf, 0xf, false);
+    return ((long long)hi << 32) | (unsigned int)lo;
+}
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_mma(const int8_t* __restrict__ kq, const float* __restrict__ sk,
+                                                  const int16_t* __restrict__ vq, int pos0, int M, int n_h, int n_kv,
+                                                  AttnScratch S, const float* __restrict__ v_scale,
+                                                  const float* __restrict__ qg, float* __restrict__ o) {
+    constexpr int KS = HD / 64;                       // 64-deep k steps of a score
+    __shared__ __attribute__((aligned(16))) int8_t kc[AM_KC * HD];
+    __shared__ float skc[AM_KC];
+    __shared__ __attribute__((aligned(16))) int8_t vt[3][AM_D][AM_KC];
+    __shared__ int ps[4][AM_T][AM_KC];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int rep = n_h / n_kv, hgroups = (rep + 3) / 4;
+    const int kvh = blockIdx.z / hgroups, hg = blockIdx.z - kvh * hgroups;
+    const int hl = hg * 4 + w, h = kvh * rep + hl;
+    const bool active = hl < rep;
+    const int t0 = blockIdx.y * AM_T, d0 = blockIdx.x * AM_D;
+    const int nk = pos0 + min(M, t0 + AM_T);          // keys any row of the block sees
+    const int c16 = lane & 15, q4 = lane >> 4;
+    // A operands of the q rows: lane holds row c16, k bytes [64 s + 16 q4, + 16)
+    v4i_t qa[KS];
+    {
+        const int t = t0 + c16;
+        const int8_t* qr = S.qq + ((size_t)t * n_h + (active ? h : 0)) * HD;
+#pragma unroll
+        for (int s2 = 0; s2 < KS; s2++)
+            qa[s2] = (active && t < M) ? *reinterpret_cast<const v4i_t*>(qr + 64 * s2 + 16 * q4) : v4i_t{0, 0, 0, 0};
+    }
+    // C layout rows of this lane: i = 4 q4 + r
+    float sqr[4];
+    int posr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int t = t0 + 4 * q4 + r;
+        const bool ok = active && t < M;
+        sqr[r] = ok ? S.sq[(size_t)t * n_h + h] : 0.0f;
+        posr[r] = ok ? pos0 + t : -1;                  // keys 0 .. posr are seen; none for a padding row
+    }
+    auto stage_k = [&](int j0) __attribute__((always_inline)) {
+        for (int e = tid; e < AM_KC * (HD / 16); e += 256) {
+            const int j = e / (HD / 16), c = e - j * (HD / 16);
+            v4i_t v = {0, 0, 0, 0};
+            if (j0 + j < nk) v = *reinterpret_cast<const v4i_t*>(kq + ((size_t)(j0 + j) * n_kv + kvh) * HD + 16 * c);
+            *reinterpret_cast<v4i_t*>(kc + j * HD + 16 * c) = v;
+        }
+        for (int j = tid; j < AM_KC; j += 256) skc[j] = j0 + j < nk ? sk[(size_t)(j0 + j) * n_kv + kvh] : 0.0f;
+    };
+    // the 16 x 16 score tile of key columns ct * 16 .. + 15 of the staged chunk
+    auto scores = [&](int ct) __attribute__((always_inline)) {
+        v4i_t acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int s2 = 0; s2 < KS; s2++) {
+            const v4i_t b = *reinterpret_cast<const v4i_t*>(kc + (ct * 16 + c16) * HD + 64 * s2 + 16 * q4);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[s2], b, acc, 0, 0, 0);
+        }
+        return acc;
+    };
+    // pass 1: row maxima
+    float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+    for (int j0 = 0; j0 < nk; j0 += AM_KC) {
+        __syncthreads();
+        stage_k(j0);
+        __syncthreads();
+        if (!active) continue;
+#pragma unroll
+        for (int ct = 0; ct < AM_KC / 16; ct++) {
+            const v4i_t acc = scores(ct);
+            const int j = j0 + ct * 16 + c16;
+            const float skj = skc[ct * 16 + c16];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (j <= posr[r]) mx[r] = fmax_spec(mx[r], ((float)acc[r] * sqr[r]) * skj);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {                     // over the 16 lanes of the row group (order-free)
+        mx[r] = fmax_spec(mx[r], dpp_f<0xB1>(mx[r]));
+        mx[r] = fmax_spec(mx[r], dpp_f<0x4E>(mx[r]));
+        mx[r] = fmax_spec(mx[r], dpp_f<0x141>(mx[r]));
+        mx[r] = fmax_spec(mx[r], dpp_f<0x140>(mx[r]));
+    }
+    // pass 2: weights, den and the digit products
+    v4i_t cacc[4][3][2];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 3; b++)
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) cacc[a][b][dt] = v4i_t{0, 0, 0, 0};
+    long long den[4] = {0, 0, 0, 0};
+    for (int j0 = 0; j0 < nk; j0 += AM_KC) {
+        __syncthreads();
+        stage_k(j0);
+        for (int e = tid; e < AM_KC * AM_D; e += 256) {
+            const int j = e / AM_D, d = e - j * AM_D;
+            const int v = j0 + j < nk ? (int)vq[((size_t)(j0 + j) * n_kv + kvh) * HD + d0 + d] : 0;
+            const int v0 = ((v + 64) & 127) - 64, r1 = (v - v0) >> 7;
+            const int v1 = ((r1 + 64) & 127) - 64, v2 = (r1 - v1) >> 7;
+            vt[0][d][j] = (int8_t)v0;
+            vt[1][d][j] = (int8_t)v1;
+            vt[2][d][j] = (int8_t)v2;
+        }
+        __syncthreads();
+        if (!active) continue;
+#pragma unroll
+        for (int ct = 0; ct < AM_KC / 16; ct++) {
+            const v4i_t acc = scores(ct);
+            const int j = j0 + ct * 16 + c16;
+            const float skj = skc[ct * 16 + c16];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int pq = 0;
+                if (j <= posr[r]) pq = (int)rint_(exp_f(((float)acc[r] * sqr[r]) * skj - mx[r]) * 16777216.0f);
+                den[r] += pq;
+                ps[w][4 * q4 + r][ct * 16 + c16] = pq;
+            }
+        }
+        // A operands of the weight digits: lane holds row c16, keys 16 q4 .. + 15 (the wave's own tile; its lanes'
+        // writes above are complete before the reads: LDS operations of a wave are performed in order)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        v4i_t pa[4];
+        {
+            const int* pr = &ps[w][c16][16 * q4];
+            uint32_t wd[4][4];
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++) {
+                uint32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t pq = (uint32_t)pr[4 * k4 + k];
+                    b0 |= (pq & 127u) << (8 * k);
+                    b1 |= ((pq >> 7) & 127u) << (8 * k);
+                    b2 |= ((pq >> 14) & 127u) << (8 * k);
+                    b3 |= (pq >> 21) << (8 * k);
+                }
+                wd[0][k4] = b0; wd[1][k4] = b1; wd[2][k4] = b2; wd[3][k4] = b3;
+            }
+#pragma unroll
+            for (int a = 0; a < 4; a++) pa[a] = v4i_t{(int)wd[a][0], (int)wd[a][1], (int)wd[a][2], (int)wd[a][3]};
+        }
+#pragma unroll
+        for (int b = 0; b < 3; b++)
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) {
+                const v4i_t vb = *reinterpret_cast<const v4i_t*>(&vt[b][dt * 16 + c16][16 * q4]);
+#pragma unroll
+                for (int a = 0; a < 4; a++) cacc[a][b][dt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[a], vb, cacc[a][b][dt], 0, 0, 0);
+            }
+    }
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {                     // den over the row group's 16 lanes (exact)
+        den[r] += dpp_ll<0xB1>(den[r]);
+        den[r] += dpp_ll<0x4E>(den[r]);
+        den[r] += dpp_ll<0x141>(den[r]);
+        den[r] += dpp_ll<0x140>(den[r]);
+    }
+    const float vs = v_scale[kvh];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int t = t0 + 4 * q4 + r;
+        if (t >= M) continue;
+        const float fden = i64_to_f(den[r]);
+        const float* gate = qg + ((size_t)t * n_h + h) * 2 * HD + HD;
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++) {
+            long long num = 0;
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 3; b++) num += (long long)cacc[a][b][dt][r] << (7 * (a + b));
+            const int d = d0 + dt * 16 + c16;
+            o[((size_t)t * n_h + h) * HD + d] = ((i64_to_f(num) / fden) * vs) * sigmoid_f(gate[d]);
+        }
+    }
+}
+
 // the output of a batch's rows once every chunk has added its sums (k_attn_acc<CK, false>)
 __global__ void __launch_bounds__(RT) k_attn_fin(const float* __restrict__ v_scale, const float* __restrict__ qg,
                                                  int n_h, int n_kv, int hd, AttnScratch S, float* __restrict__ o) {
@@ -709,6 +904,19 @@ void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float*
         k_attn_max<32><<<grid, RT, 0, st>>>(kv->kq, kv->sk, pos0, n_h, n_kv, hd, S);
         DET_CHECK(hipGetLastError());
         k_attn_acc<32, true><<<grid, RT, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, n_h, n_kv, hd, S, L->v_scale, qg, o);
+    } else if (hd == 256 && (long long)nkeys < (1 << 18)) {
+        // a batch: the matrix-core path (workgroups of 32 dims x 16 tokens x up to 4 heads of a kv head)
+        const int rep = n_h / n_kv;
+        const dim3 grid(hd / AM_D, (M + AM_T - 1) / AM_T, n_kv * ((rep + 3) / 4));
+        k_attn_mma<256><<<grid, 256, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, M, n_h, n_kv, S, L->v_scale, qg, o);
+    } else if (hd == 128 && (long long)nkeys < (1 << 18)) {
+        const int rep = n_h / n_kv;
+        const dim3 grid(hd / AM_D, (M + AM_T - 1) / AM_T, n_kv * ((rep + 3) / 4));
+        k_attn_mma<128><<<grid, 256, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, M, n_h, n_kv, S, L->v_scale, qg, o);
+    } else if (hd == 64 && (long long)nkeys < (1 << 18)) {
+        const int rep = n_h / n_kv;
+        const dim3 grid(hd / AM_D, (M + AM_T - 1) / AM_T, n_kv * ((rep + 3) / 4));
+        k_attn_mma<64><<<grid, 256, 0, st>>>(kv->kq, kv->sk, kv->vq, pos0, M, n_h, n_kv, S, L->v_scale, qg, o);
     } else {
         const dim3 grid((nkeys + 255) / 256, M * n_h);
         k_attn_max<256><<<grid, RT, 0, st>>>(kv->kq, kv->sk, pos0, n_h, n_kv, hd, S);
