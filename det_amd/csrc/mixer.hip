@@ -581,6 +581,70 @@ __global__ void __launch_bounds__(RT) k_gdn_prep(const float* __restrict__ y, co
     }
 }
 
+// ---- row kernels of a batch, one wave per row: the row's n <= 64 EPT values sit in registers, EPT consecutive per
+// lane, so the spec's treesum of squares is each lane's aligned subtree, then lane pairs (DPP, two shuffles); leaves
+// past n (to the wave's 64 EPT) are +0 and squares are >= +0, so the root equals the tree over the padded row.
+template <int EPT>
+__device__ __forceinline__ float wave_sumsq(const float* v) {
+    float r[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; k++) r[k] = v[k] * v[k];
+#pragma unroll
+    for (int w2 = EPT >> 1; w2 >= 1; w2 >>= 1)
+#pragma unroll
+        for (int k = 0; k < w2; k++) r[k] = r[2 * k] + r[2 * k + 1];
+    float t = lane_tree_sum<16>(r[0]);
+    t = t + __shfl_xor(t, 16, 64);
+    return t + __shfl_xor(t, 32, 64);
+}
+// k_gdn_prep with a wave per (token, k head): l2norm of q (times QSCALE) and of k, beta and decay of the rep v heads
+template <int EPT>
+__global__ void __launch_bounds__(256) k_gdn_prep_w(const float* __restrict__ y, const float* __restrict__ A,
+                                                    const float* __restrict__ dt_bias, const float* __restrict__ a,
+                                                    const float* __restrict__ b, float eps, int rows, int n_k, int n_v,
+                                                    int dk, int cd, float* __restrict__ qb, float* __restrict__ kb,
+                                                    float* __restrict__ bd) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;                           // whole waves: no barrier follows
+    const int tok = row / n_k, kh = row - tok * n_k, rep = n_v / n_k;
+    const float qscale = __uint_as_float(0x3DB504F3u);            // spec/layers.rs:146
+    for (int part = 0; part < 2; part++) {
+        const float* src = y + (size_t)tok * cd + (size_t)part * n_k * dk + (size_t)kh * dk;
+        float v[EPT];
+#pragma unroll
+        for (int k = 0; k < EPT; k++) v[k] = lane * EPT + k < dk ? src[lane * EPT + k] : 0.0f;
+        const float inv = 1.0f / __builtin_sqrtf(wave_sumsq<EPT>(v) + eps);     // spec/prim.rs:183-190
+        float* dst = (part == 0 ? qb : kb) + ((size_t)tok * n_k + kh) * dk;
+#pragma unroll
+        for (int k = 0; k < EPT; k++)
+            if (lane * EPT + k < dk) dst[lane * EPT + k] = part == 0 ? (v[k] * inv) * qscale : v[k] * inv;
+    }
+    for (int i = lane; i < rep; i += 64) {
+        const int hv = kh * rep + i;
+        const size_t ti = (size_t)tok * n_v + hv;
+        bd[2 * ti] = sigmoid_f(b[ti]);
+        bd[2 * ti + 1] = exp_f(-(A[hv] * softplus_f(a[ti] + dt_bias[hv])));
+    }
+}
+// k_gdn_out with a wave per (token, v head): on = rmsnorm(o, norm) * silu(z)
+template <int EPT>
+__global__ void __launch_bounds__(256) k_gdn_out_w(const float* __restrict__ ob, const float* __restrict__ norm,
+                                                   const float* __restrict__ z, float eps, int rows, int dv,
+                                                   float* __restrict__ on) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const size_t base = (size_t)row * dv;
+    float v[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; k++) v[k] = lane * EPT + k < dv ? ob[base + lane * EPT + k] : 0.0f;
+    const float inv = 1.0f / __builtin_sqrtf((wave_sumsq<EPT>(v) / (float)dv) + eps);   // spec/prim.rs:172-181
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int i = lane * EPT + k;
+        if (i < dv) on[base + i] = ((v[k] * inv) * norm[i]) * silu_f(z[base + i]);
+    }
+}
+
 // balanced tree over the RB values of v (adjacent pairs level by level): the aligned subtree of the spec's tree
 template <int RB>
 __device__ __forceinline__ float reg_tree(float* v) {
@@ -973,7 +1037,10 @@ void gdn_run(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
         DET_CHECK(hipGetLastError());
         int p = 1;
         while (p < dk) p <<= 1;
-        k_gdn_prep<<<M * n_k, RT, ((size_t)dk + p + p / 2) * 4, st>>>(y, L->A, L->dt_bias, a, b, eps, n_k, n_v, dk, cd, qb, kb, bd);
+        const int rows = M * n_k, wg = (rows + 3) / 4;
+        (void)p;
+        if (dk <= 64) k_gdn_prep_w<1><<<wg, 256, 0, st>>>(y, L->A, L->dt_bias, a, b, eps, rows, n_k, n_v, dk, cd, qb, kb, bd);
+        else k_gdn_prep_w<2><<<wg, 256, 0, st>>>(y, L->A, L->dt_bias, a, b, eps, rows, n_k, n_v, dk, cd, qb, kb, bd);
         DET_CHECK(hipGetLastError());
     }
     // lanes per column: 16 (dk when dk < 16); blocks of GT / R columns, one workgroup each (grid y)
@@ -997,9 +1064,10 @@ void gdn_run(const det_gdn_layer* L, det_gdn_state* S, const float* qkv, const f
     }
     DET_CHECK(hipGetLastError());
     if (cnt) return;                                  // one token: the recurrence's last block of each head ran the gated norm
-    int pv = 1;
-    while (pv < dv) pv <<= 1;
-    k_gdn_out<<<M * n_v, RT, ((size_t)dv + pv + pv / 2) * 4, st>>>(ob, L->norm, z, eps, dv, on);
+    const int rows = M * n_v, wg = (rows + 3) / 4;
+    if (dv <= 64) k_gdn_out_w<1><<<wg, 256, 0, st>>>(ob, L->norm, z, eps, rows, dv, on);
+    else if (dv <= 128) k_gdn_out_w<2><<<wg, 256, 0, st>>>(ob, L->norm, z, eps, rows, dv, on);
+    else k_gdn_out_w<4><<<wg, 256, 0, st>>>(ob, L->norm, z, eps, rows, dv, on);
     DET_CHECK(hipGetLastError());
 }
 
