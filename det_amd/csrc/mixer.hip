@@ -309,6 +309,106 @@ __global__ void __launch_bounds__(RT) k_attn_acc(const int8_t* __restrict__ kq, 
 }
 
 
+// ---- row kernels of a batch, one wave per row: the row's n <= 64 EPT values sit in registers, EPT consecutive per
+// lane, so the spec's treesum of squares is each lane's aligned subtree, then lane pairs (DPP, two shuffles); leaves
+// past n (to the wave's 64 EPT) are +0 and squares are >= +0, so the root equals the tree over the padded row.
+template <int EPT>
+__device__ __forceinline__ float wave_sumsq(const float* v) {
+    float r[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; k++) r[k] = v[k] * v[k];
+#pragma unroll
+    for (int w2 = EPT >> 1; w2 >= 1; w2 >>= 1)
+#pragma unroll
+        for (int k = 0; k < w2; k++) r[k] = r[2 * k] + r[2 * k + 1];
+    float t = lane_tree_sum<16>(r[0]);
+    t = t + __shfl_xor(t, 16, 64);
+    return t + __shfl_xor(t, 32, 64);
+}
+// k_attn_prep with a wave per row for hd = 64 EPT (EPT = 1, 2, 4): the row in registers, EPT consecutive values
+// per lane; the RMSNorm sum by lane subtrees and DPP (the spec's tree: hd is a power of two), rope's partner
+// values (i +- half, half a multiple of EPT) by a lane shuffle, the absmax by DPP.  Same operations as
+// attn_kv_row / attn_q_row.
+template <int EPT>
+__device__ __forceinline__ float wave_absmax0(const float* v) {
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < EPT; k++) am = fmax_spec(am, __builtin_fabsf(v[k]));
+    return wave_fmax(am);
+}
+template <int EPT>
+__device__ __forceinline__ void wave_norm_rope(float* v, const float* __restrict__ nw, float eps, const float* cs,
+                                               const float* sn, int half, int lane) {
+    constexpr int HD = 64 * EPT;
+    const float inv = 1.0f / __builtin_sqrtf((wave_sumsq<EPT>(v) / (float)HD) + eps);   // spec/prim.rs:172-181
+#pragma unroll
+    for (int k = 0; k < EPT; k++) v[k] = (v[k] * inv) * nw[lane * EPT + k];
+    const int sh = half / EPT;                                   // lanes between i and i + half
+    const bool lo = lane * EPT < half, hi = lane * EPT >= half && lane * EPT < 2 * half;
+    const int src = lo ? lane + sh : hi ? lane - sh : lane;
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {                              // spec/layers.rs:5-13
+        const float pv = __shfl(v[k], src, 64);
+        const int i = lane * EPT + k;
+        if (lo) v[k] = (v[k] * cs[i]) - (pv * sn[i]);
+        else if (hi) v[k] = (v[k] * cs[i - half]) + (pv * sn[i - half]);
+    }
+}
+template <int EPT>
+__global__ void __launch_bounds__(256) k_attn_prep_w(const float* __restrict__ k_norm, const float* __restrict__ v_inv_scale,
+                                                     int8_t* __restrict__ kq, float* __restrict__ sk, int16_t* __restrict__ vq,
+                                                     const float* __restrict__ k, const float* __restrict__ v,
+                                                     const float* __restrict__ q_norm, const float* __restrict__ qg,
+                                                     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+                                                     int half, float eps, int pos0, int n_kv, int n_h, int nkv, int nrows,
+                                                     AttnScratch S) {
+    constexpr int HD = 64 * EPT;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= nrows) return;                          // whole waves; no barrier follows
+    float x[EPT];
+    if (row < nkv) {
+        const int tok = row / n_kv, h = row - tok * n_kv, pos = pos0 + tok;
+        const size_t src = ((size_t)tok * n_kv + h) * HD;
+#pragma unroll
+        for (int e = 0; e < EPT; e++) x[e] = k[src + lane * EPT + e];
+        wave_norm_rope<EPT>(x, k_norm, eps, rope_cos + (size_t)pos * half, rope_sin + (size_t)pos * half, half, lane);
+        const float am = wave_absmax0<EPT>(x);
+        const float sc = am == 0.0f ? 1.0f : am / 127.0f, inv = 1.0f / sc;          // spec/quant.rs:8-16
+        const size_t dst = ((size_t)pos * n_kv + h) * HD;
+#pragma unroll
+        for (int e = 0; e < EPT; e++) kq[dst + lane * EPT + e] = (int8_t)clamp_i8(rint_(x[e] * inv));
+        if (lane == 0) sk[(size_t)pos * n_kv + h] = sc;
+        const float vi = v_inv_scale[h];
+#pragma unroll
+        for (int e = 0; e < EPT; e++) {                                              // spec/layers.rs:73-86
+            const float r = rint_(v[src + lane * EPT + e] * vi);
+            vq[dst + lane * EPT + e] = (int16_t)(r < -32767.0f ? -32767 : r > 32767.0f ? 32767 : __builtin_isnan(r) ? 0 : (int)r);
+        }
+        return;
+    }
+    const int qrow = row - nkv, tok = qrow / n_h, pos = pos0 + tok;
+    const float* qr = qg + (size_t)qrow * 2 * HD;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) x[e] = qr[lane * EPT + e];
+    wave_norm_rope<EPT>(x, q_norm, eps, rope_cos + (size_t)pos * half, rope_sin + (size_t)pos * half, half, lane);
+    const float qscale = 1.0f / __builtin_sqrtf((float)HD);
+#pragma unroll
+    for (int e = 0; e < EPT; e++) x[e] = x[e] * qscale;
+    const float am = wave_absmax0<EPT>(x);
+    const float sq = am == 0.0f ? 1.0f : am / 127.0f, inv = 1.0f / sq;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        S.qq[(size_t)qrow * HD + lane * EPT + e] = (int8_t)clamp_i8(rint_(x[e] * inv));
+        S.num[(size_t)qrow * HD + lane * EPT + e] = 0;
+    }
+    if (lane == 0) {
+        S.sq[qrow] = sq;
+        S.mxo[qrow] = 0u;
+        S.den[qrow] = 0;
+        S.cnt[qrow] = 0u;
+    }
+}
+
 // ---- a batch on the matrix cores (k_attn_mma): the same integers and fp32 operations as k_attn_max / k_attn_acc.
 // Workgroup = (32 output dims, 16 tokens, up to 4 q heads of one kv head: a wave each); keys in chunks of 64 staged
 // in LDS and shared by the heads.  Scores: v_mfma_i32_16x16x64_i8 of the int8 q rows by the int8 key rows (exact
@@ -581,22 +681,7 @@ __global__ void __launch_bounds__(RT) k_gdn_prep(const float* __restrict__ y, co
     }
 }
 
-// ---- row kernels of a batch, one wave per row: the row's n <= 64 EPT values sit in registers, EPT consecutive per
-// lane, so the spec's treesum of squares is each lane's aligned subtree, then lane pairs (DPP, two shuffles); leaves
-// past n (to the wave's 64 EPT) are +0 and squares are >= +0, so the root equals the tree over the padded row.
-template <int EPT>
-__device__ __forceinline__ float wave_sumsq(const float* v) {
-    float r[EPT];
-#pragma unroll
-    for (int k = 0; k < EPT; k++) r[k] = v[k] * v[k];
-#pragma unroll
-    for (int w2 = EPT >> 1; w2 >= 1; w2 >>= 1)
-#pragma unroll
-        for (int k = 0; k < w2; k++) r[k] = r[2 * k] + r[2 * k + 1];
-    float t = lane_tree_sum<16>(r[0]);
-    t = t + __shfl_xor(t, 16, 64);
-    return t + __shfl_xor(t, 32, 64);
-}
+// ---- row kernels of a batch, one wave per row (wave_sumsq above)
 // k_gdn_prep with a wave per (token, k head): l2norm of q (times QSCALE) and of k, beta and decay of the rep v heads
 template <int EPT>
 __global__ void __launch_bounds__(256) k_gdn_prep_w(const float* __restrict__ y, const float* __restrict__ A,
@@ -958,6 +1043,16 @@ void det_attention(const det_attn_layer* L, const det_kv_cache* kv, const float*
     while (p < hd) p <<= 1;
     const size_t lds_row = ((size_t)hd + p + p / 2) * 4;
     const AttnScratch S = attn_layout(scratch, M, n_h, hd);
+    const int nrows = M * (n_kv + n_h), half = rot / 2;
+    const int ept = hd == 256 ? 4 : hd == 128 ? 2 : hd == 64 ? 1 : 0;
+    if (ept && half % ept == 0) {
+        if (ept == 4) k_attn_prep_w<4><<<(nrows + 3) / 4, 256, 0, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, L->q_norm, qg,
+                                                                       rope_cos, rope_sin, half, eps, pos0, n_kv, n_h, M * n_kv, nrows, S);
+        else if (ept == 2) k_attn_prep_w<2><<<(nrows + 3) / 4, 256, 0, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, L->q_norm, qg,
+                                                                            rope_cos, rope_sin, half, eps, pos0, n_kv, n_h, M * n_kv, nrows, S);
+        else k_attn_prep_w<1><<<(nrows + 3) / 4, 256, 0, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, L->q_norm, qg,
+                                                              rope_cos, rope_sin, half, eps, pos0, n_kv, n_h, M * n_kv, nrows, S);
+    } else
     k_attn_prep<<<M * (n_kv + n_h), RT, lds_row, st>>>(L->k_norm, L->v_inv_scale, kv->kq, kv->sk, kv->vq, k, v, L->q_norm, qg,
                                                       rope_cos, rope_sin, rot / 2, eps, pos0, n_kv, n_h, hd, M * n_kv, S);
     DET_CHECK(hipGetLastError());
