@@ -71,6 +71,11 @@ def test_attention_4b_shape_decode_over_many_key_chunks():
     check_attention(16, 4, 256, 64, [300, 1, 1, 3, 200, 1], 600, seed=6)
 
 
+def test_attention_head_dim_128_batches():
+    """hd = 128: the matrix-core batch path and the wave-per-row prep at two lanes' values each, GQA rep 4."""
+    check_attention(8, 2, 128, 32, [40, 1, 7, 70], 128, seed=7)
+
+
 def test_attention_long_prefill_chunks():
     """More than one 1024-key chunk in the weight pass, and the last cache row."""
     check_attention(2, 1, 64, 16, [1100, 1], 1101, seed=2)
@@ -116,7 +121,7 @@ def test_gdn_4b_shape_prefill_then_decode():
 
 
 @pytest.mark.parametrize('n_k,n_v,dk,dv', [(1, 2, 4, 4), (2, 4, 8, 16), (1, 2, 16, 8), (1, 1, 32, 24),
-                                           (2, 2, 64, 40), (1, 1, 128, 20)])
+                                           (2, 2, 64, 40), (1, 1, 128, 20), (1, 2, 64, 256)])
 def test_gdn_small_shapes(n_k, n_v, dk, dv):
     # 33 and 64 tokens span two token chunks of the recurrence (a partial and a full second one)
     check_gdn(n_k, n_v, dk, dv, [1, 2, 5, 33, 64, 1], seed=5)
