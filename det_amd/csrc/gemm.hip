@@ -24,6 +24,7 @@
 #include <string.h>
 #include <algorithm>
 #include "common.h"
+#include "gemm_internal.h"
 #include "../../include/det_hip.h"
 using namespace det;
 
@@ -36,6 +37,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 struct Out {
     float* y;
     int acc, nparts;
+    int silu0;           // values routed to part 0 become silu_f(v) (one-token gate|up: cpu.rs:187-211's silu of g)
     int offs[5];
     float* dst[4];
     __device__ __forceinline__ float* ptr(int N, int t, int n) const {
@@ -49,6 +51,7 @@ struct Out {
         return d + (size_t)t * (hi - lo) + (n - lo);
     }
     __device__ __forceinline__ void store(int N, int t, int n, float v) const {
+        if (silu0 && n < offs[1]) v = silu_f(v);
         float* p = ptr(N, t, n);
         *p = acc ? *p + v : v;
     }
@@ -1362,3 +1365,32 @@ void det_gemm(const det_qlinear* Lp, const int8_t* xq, const float* sx, const ui
 }
 
 } // extern "C"
+
+namespace det {
+
+void gemm_parts_silu0(const det_qlinear* Lp, const int8_t* xq, const float* sx, const uint16_t* mx, int nparts,
+                      const int* offs, float* const* dsts, hipStream_t st) {
+    const det_qlinear L = *Lp;
+    if (nparts < 2 || nparts > 4 || offs[0] != 0) DET_FAIL("det_gemm: silu of part 0 needs 2 to 4 parts from column 0");
+    if (L.K % GROUP != 0 || L.K <= 0 || L.N <= 0) DET_FAIL("det_gemm: bad shape N=%d K=%d", L.N, L.K);
+    if (L.bits != 4 && L.bits != 6 && L.bits != 8) DET_FAIL("det_gemm: unsupported bits=%d", L.bits);
+    if (g_num_cus == 0) {
+        int dev = 0;
+        DET_CHECK(hipGetDevice(&dev));
+        DET_CHECK(hipDeviceGetAttribute(&g_num_cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_decode_waves = 8 * g_num_cus;
+    }
+    Out out;
+    memset(&out, 0, sizeof out);
+    out.nparts = nparts;
+    out.silu0 = 1;
+    for (int i = 0; i < nparts; i++) { out.dst[i] = dsts[i]; out.offs[i] = offs[i]; }
+    out.offs[nparts] = L.N;
+    switch (L.bits) {                              // one token: the GEMV, whose epilogue goes through Out::store
+        case 8: launch_decode<8, 1>(L, xq, sx, mx, 1, out, st); break;
+        case 6: launch_decode<6, 1>(L, xq, sx, mx, 1, out, st); break;
+        default: launch_decode<4, 1>(L, xq, sx, mx, 1, out, st); break;
+    }
+}
+
+} // namespace det

@@ -7,6 +7,7 @@
 #include "common.h"
 #include "gguf_reader.h"
 #include "mixer_internal.h"
+#include "gemm_internal.h"
 #include "../../include/det_hip.h"
 #include "../../include/det_model.h"
 
@@ -335,8 +336,17 @@ void forward_layers(det_model* m, int pos0, int t) {
             det_gemm_ex(&L.g.out.lins[0].q, m->onq, m->son, m->mon, t, m->x, 1, 0, nullptr, nullptr, st);
         }
         det_rmsnorm_quant(m->x, L.ffn_norm, eps, t, h, nullptr, m->xq, m->sx, m->mx, st);
-        m->project(L.gu, m->xq, m->sx, m->mx, t, {m->gg, m->u});
-        det_silu_mul_quant(m->gg, m->u, t, (int)c.intermediate, nullptr, m->hq, m->sh, m->mh, st);
+        // one token through one fused gate|up linear: the GEMV stores silu(g), and the quantization only multiplies
+        const int ff = (int)c.intermediate;
+        if (t == 1 && L.gu.lins.size() == 1 && L.gu.lins[0].widths.size() == 2 && ff % 128 == 0 && ff <= 32768) {
+            const int offs[2] = {0, L.gu.lins[0].widths[0]};
+            float* ds[2] = {m->gg, m->u};
+            det::gemm_parts_silu0(&L.gu.lins[0].q, m->xq, m->sx, m->mx, 2, offs, ds, st);
+            if (!det::mul_quant(m->gg, m->u, 1, ff, m->hq, m->sh, m->mh, st)) throw Error("mul_quant: unsupported row");
+        } else {
+            m->project(L.gu, m->xq, m->sx, m->mx, t, {m->gg, m->u});
+            det_silu_mul_quant(m->gg, m->u, t, ff, nullptr, m->hq, m->sh, m->mh, st);
+        }
         det_gemm_ex(&L.down.lins[0].q, m->hq, m->sh, m->mh, t, m->x, 1, 0, nullptr, nullptr, st);
     }
     // the last token's row only (qwen35.rs:157-170)

@@ -5,6 +5,7 @@
 // code becomes 0.
 #include <string.h>
 #include "common.h"
+#include "gemm_internal.h"
 #include "../../include/det_hip.h"
 using namespace det;
 
@@ -14,7 +15,7 @@ namespace {
 // waves to overlap its latency-bound reductions); the results do not depend on the count
 constexpr int QT_MANY = 256, QT_FEW = 1024, QT_FEW_MAX_ROWS = 64;
 
-enum { MODE_QUANT = 0, MODE_RMSNORM = 1, MODE_SILU_MUL = 2 };
+enum { MODE_QUANT = 0, MODE_RMSNORM = 1, MODE_SILU_MUL = 2, MODE_MUL = 3 };
 
 __host__ __device__ __forceinline__ int p_of(int n) { int p = 1; while (p < n) p <<= 1; return p; }
 
@@ -212,6 +213,10 @@ __global__ void __launch_bounds__(1024) k_qrow(const float* __restrict__ a, cons
 #pragma unroll
         for (int k = 0; k < EPT; k++) v[k] = silu_f(v[k]) * u[k];
     }
+    if (MODE == MODE_MUL) {
+#pragma unroll
+        for (int k = 0; k < EPT; k++) v[k] = v[k] * u[k];
+    }
     if (MODE == MODE_RMSNORM) {
         float sq[EPT];
 #pragma unroll
@@ -332,3 +337,12 @@ void det_silu_mul_quant(const float* g, const float* u, int M, int n, float* h, 
 }
 
 } // extern "C"
+
+namespace det {
+
+bool mul_quant(const float* a, const float* b, int M, int n, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st) {
+    if (M < 1) return true;
+    return launch_qrow<MODE_MUL>(a, b, 0.0f, M, n, nullptr, xq, sx, mx, st);
+}
+
+} // namespace det
