@@ -37,7 +37,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 struct Out {
     float* y;
     int acc, nparts;
-    int silu0;           // values routed to part 0 become silu_f(v) (one-token gate|up: cpu.rs:187-211's silu of g)
     int offs[5];
     float* dst[4];
     __device__ __forceinline__ float* ptr(int N, int t, int n) const {
@@ -51,7 +50,6 @@ struct Out {
         return d + (size_t)t * (hi - lo) + (n - lo);
     }
     __device__ __forceinline__ void store(int N, int t, int n, float v) const {
-        if (silu0 && n < offs[1]) v = silu_f(v);
         float* p = ptr(N, t, n);
         *p = acc ? *p + v : v;
     }
@@ -219,7 +217,14 @@ __device__ __forceinline__ int dec_row(int r, int lane) {
 template <int MP>
 constexpr int dec_maxw() { return MP >= DEC_MMA_MIN ? 8 : DEC_MAXW; }     // the matrix-core form needs up to 256 VGPRs
 
-template <int BITS, int MP>
+// SILU0: the one-token gate|up projection stores silu_f(v) for the columns of part 0 (cpu.rs:187-211's silu of g)
+template <bool SILU0>
+__device__ __forceinline__ float dec_val(const Out& out, int n, float v) {
+    if constexpr (SILU0) return n < out.offs[1] ? silu_f(v) : v;
+    return v;
+}
+
+template <int BITS, int MP, bool SILU0 = false>
 __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
                                                 const uint16_t* __restrict__ ms, int N, int K,
                                                 const int8_t* __restrict__ xq, const float* __restrict__ sx,
@@ -329,7 +334,7 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
 #pragma unroll
         for (int r = 0; r < MP; r++) {
             const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
-            if (t < M && n < N) out.store(N, t, n, (i64_to_f(acc[r]) * csr[r]) * sxr[r]);
+            if (t < M && n < N) out.store(N, t, n, dec_val<SILU0>(out, n, (i64_to_f(acc[r]) * csr[r]) * sxr[r]));
         }
         return;
     }
@@ -372,7 +377,7 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
 #pragma unroll
     for (int r = 0; r < MP; r++) {
         const int t = dec_tok<MP>(r, lane), n = tile * TILE_N + dec_row<MP>(r, lane);
-        if (r % S == wv && t < M && n < N) out.store(N, t, n, (i64_to_f(tot[r]) * csr[r]) * sxr[r]);
+        if (r % S == wv && t < M && n < N) out.store(N, t, n, dec_val<SILU0>(out, n, (i64_to_f(tot[r]) * csr[r]) * sxr[r]));
     }
 }
 
@@ -1173,7 +1178,7 @@ void decode_buffers(size_t part_elems, size_t tiles, hipStream_t st) {
     DET_CHECK(hipDeviceSynchronize());
 }
 
-template <int BITS, int MP>
+template <int BITS, int MP, bool SILU0 = false>
 void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, const Out& y, hipStream_t st) {
     const int G = L.K / GROUP;
     const int T = (L.N + TILE_N - 1) / TILE_N;
@@ -1193,7 +1198,7 @@ void launch_decode(const det_qlinear& L, const int8_t* xq, const float* sx, cons
         cnt = g_cnt;
     }
     const size_t lds = S > 1 ? (size_t)S * MP * 64 * sizeof(long long) : 0;
-    k_decode<BITS, MP><<<T * KS, 64 * S, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
+    k_decode<BITS, MP, SILU0><<<T * KS, 64 * S, lds, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, KS, part, cnt);
     DET_CHECK(hipGetLastError());
 }
 
@@ -1383,13 +1388,12 @@ void gemm_parts_silu0(const det_qlinear* Lp, const int8_t* xq, const float* sx, 
     Out out;
     memset(&out, 0, sizeof out);
     out.nparts = nparts;
-    out.silu0 = 1;
     for (int i = 0; i < nparts; i++) { out.dst[i] = dsts[i]; out.offs[i] = offs[i]; }
     out.offs[nparts] = L.N;
     switch (L.bits) {                              // one token: the GEMV, whose epilogue goes through Out::store
-        case 8: launch_decode<8, 1>(L, xq, sx, mx, 1, out, st); break;
-        case 6: launch_decode<6, 1>(L, xq, sx, mx, 1, out, st); break;
-        default: launch_decode<4, 1>(L, xq, sx, mx, 1, out, st); break;
+        case 8: launch_decode<8, 1, true>(L, xq, sx, mx, 1, out, st); break;
+        case 6: launch_decode<6, 1, true>(L, xq, sx, mx, 1, out, st); break;
+        default: launch_decode<4, 1, true>(L, xq, sx, mx, 1, out, st); break;
     }
 }
 
