@@ -25,159 +25,11 @@
 #include <algorithm>
 #include "common.h"
 #include "gemm_internal.h"
+#include "gemm_common.h"
 #include "../../include/det_hip.h"
 using namespace det;
 
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-// ------------------------------------------------------------------ output routing (GemmOut, backend.rs:138-142)
-struct Out {
-    float* y;
-    int acc, nparts;
-    int offs[5];
-    float* dst[4];
-    __device__ __forceinline__ float* ptr(int N, int t, int n) const {
-        if (nparts <= 1) return y + (size_t)t * N + n;
-        // selects, not an indexed load: a runtime index into dst/offs would put the struct in private memory
-        float* d = dst[0];
-        int lo = offs[0], hi = offs[1];
-#pragma unroll
-        for (int j = 1; j < 4; j++)
-            if (j < nparts && n >= offs[j]) { d = dst[j]; lo = offs[j]; hi = offs[j + 1]; }
-        return d + (size_t)t * (hi - lo) + (n - lo);
-    }
-    __device__ __forceinline__ void store(int N, int t, int n, float v) const {
-        float* p = ptr(N, t, n);
-        *p = acc ? *p + v : v;
-    }
-};
-
-// ------------------------------------------------------------------ code unpacking
-// One 32-code block of the det format (spec §2): W8 = 8 words of int8; W4 = 4 words, byte i = u[i] | u[i+16] << 4
-// with u = wq + 8; W6 = 4 words of low nibbles as W4 (u = wq + 32) then 2 words of 2-bit high parts, byte i =
-// hi[i] | hi[i+8] << 2 | hi[i+16] << 4 | hi[i+24] << 6.  Output: 8 words of signed codes in k order.
-// Unsigned bytes u in [0, 2^b) become signed u - OFF per byte as (u + 128 - OFF) ^ 0x80 (no carry between bytes).
-template <int BITS> __device__ __forceinline__ void block_signed(const uint32_t* q, uint32_t* s);
-template <> __device__ __forceinline__ void block_signed<8>(const uint32_t* q, uint32_t* s) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) s[j] = q[j];
-}
-template <> __device__ __forceinline__ void block_signed<4>(const uint32_t* q, uint32_t* s) {
-    constexpr uint32_t LM = 0x0F0F0F0Fu, ADD = 0x78787878u, X = 0x80808080u;   // 120 = 128 - 8
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        s[j] = ((q[j] & LM) + ADD) ^ X;
-        s[j + 4] = (((q[j] >> 4) & LM) + ADD) ^ X;
-    }
-}
-template <> __device__ __forceinline__ void block_signed<6>(const uint32_t* q, uint32_t* s) {
-    constexpr uint32_t LM = 0x0F0F0F0Fu, HM = 0x30303030u, ADD = 0x60606060u, X = 0x80808080u;  // 96 = 128 - 32
-    // codes 4j..4j+3: low nibble from word j % 4 (high half for j >= 4); the high pair sits at bit 2*(j/2 % 4)... of
-    // high word (j & 1): codes c = 4j + b keep their pair in high byte (c % 8) at shift 2 * (c / 8)
-    const uint32_t h0 = q[4], h1 = q[5];
-    uint32_t u[8];
-    u[0] = (q[0] & LM) | ((h0 << 4) & HM);
-    u[1] = (q[1] & LM) | ((h1 << 4) & HM);
-    u[2] = (q[2] & LM) | ((h0 << 2) & HM);
-    u[3] = (q[3] & LM) | ((h1 << 2) & HM);
-    u[4] = ((q[0] >> 4) & LM) | (h0 & HM);
-    u[5] = ((q[1] >> 4) & LM) | (h1 & HM);
-    u[6] = ((q[2] >> 4) & LM) | ((h0 >> 2) & HM);
-    u[7] = ((q[3] >> 4) & LM) | ((h1 >> 2) & HM);
-#pragma unroll
-    for (int j = 0; j < 8; j++) s[j] = (u[j] + ADD) ^ X;
-}
-
-// One 32-code block as unsigned codes u = wq + OFF (W4: 0..15, W6: 0..63), 8 words in k order.  These are valid
-// non-negative int8 operands; the -OFF part of the codes is applied separately (on the MFMA, as x . (-OFF)).
-template <int BITS> __device__ __forceinline__ void block_unsigned(const uint32_t* q, uint32_t* u);
-template <> __device__ __forceinline__ void block_unsigned<4>(const uint32_t* q, uint32_t* u) {
-    constexpr uint32_t LM = 0x0F0F0F0Fu;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        u[j] = q[j] & LM;
-        u[j + 4] = (q[j] >> 4) & LM;
-    }
-}
-template <> __device__ __forceinline__ void block_unsigned<6>(const uint32_t* q, uint32_t* u) {
-    constexpr uint32_t LM = 0x0F0F0F0Fu, HM = 0x30303030u;
-    const uint32_t h0 = q[4], h1 = q[5];
-    u[0] = (q[0] & LM) | ((h0 << 4) & HM);
-    u[1] = (q[1] & LM) | ((h1 << 4) & HM);
-    u[2] = (q[2] & LM) | ((h0 << 2) & HM);
-    u[3] = (q[3] & LM) | ((h1 << 2) & HM);
-    u[4] = ((q[0] >> 4) & LM) | (h0 & HM);
-    u[5] = ((q[1] >> 4) & LM) | (h1 & HM);
-    u[6] = ((q[2] >> 4) & LM) | ((h0 >> 2) & HM);
-    u[7] = ((q[3] >> 4) & LM) | ((h1 >> 2) & HM);
-}
-template <> __device__ __forceinline__ void block_unsigned<8>(const uint32_t* q, uint32_t* u) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) u[j] = q[j];
-}
-
-// ------------------------------------------------------------------ global -> LDS copies
-// Global -> LDS copy by the buffer unit (BYTES = 4 or 16 per lane, lane i's bytes land at lds + i * BYTES), written as
-// inline assembly so that the compiler does not track it: with the builtin it cannot tell that later LDS reads touch
-// other buffers and waits for every copy in flight before the first of them.  The caller waits (s_waitcnt vmcnt)
-// and synchronises before reading the target.  `lds` must be wave-uniform.
-template <int BYTES>
-__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff_, const void* lds) {
-    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    if (BYTES == 16)
-        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
-    else
-        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
-}
-
-// N (<= 4) copies of 16 bytes per lane under one M0 value: copy i reads the resource at voff[i] + soff + 1024 i and
-// lands at lds + 1024 i + 16 lane (the instruction offset moves both addresses).  Changing M0 stalls until the copies
-// issued before have consumed it, so each run sets it once.
-template <int N>
-__device__ __forceinline__ void dma16_run(__amdgpu_buffer_rsrc_t r, const uint32_t* voff, uint32_t soff_, const void* lds) {
-    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);      // uniform by construction; keep it scalar
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    static_assert(N >= 1 && N <= 4, "at most 4 copies per run");
-    if constexpr (N == 4)
-        asm volatile("s_mov_b32 m0, %5\n\t"
-                     "buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
-                     "buffer_load_dwordx4 %1, %4, %6 offen offset:1024 lds\n\t"
-                     "buffer_load_dwordx4 %2, %4, %6 offen offset:2048 lds\n\t"
-                     "buffer_load_dwordx4 %3, %4, %6 offen offset:3072 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-    else if constexpr (N == 3)
-        asm volatile("s_mov_b32 m0, %4\n\t"
-                     "buffer_load_dwordx4 %0, %3, %5 offen lds\n\t"
-                     "buffer_load_dwordx4 %1, %3, %5 offen offset:1024 lds\n\t"
-                     "buffer_load_dwordx4 %2, %3, %5 offen offset:2048 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-    else if constexpr (N == 2)
-        asm volatile("s_mov_b32 m0, %3\n\t"
-                     "buffer_load_dwordx4 %0, %2, %4 offen lds\n\t"
-                     "buffer_load_dwordx4 %1, %2, %4 offen offset:1024 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-    else
-        asm volatile("s_mov_b32 m0, %2\n\t"
-                     "buffer_load_dwordx4 %0, %1, %3 offen lds"
-                     :: "v"(voff[0]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
-}
-// four copies under one M0, copy i through resource r[i] at voff[i % 2] + soff + 1024 i, landing at
-// lds + 1024 i + 16 lane
-__device__ __forceinline__ void dma16_run4x(const __amdgpu_buffer_rsrc_t* r, uint32_t voff0, uint32_t voff1, uint32_t soff_,
-                                            const void* lds) {
-    const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    asm volatile("s_mov_b32 m0, %6\n\t"
-                 "buffer_load_dwordx4 %0, %2, %7 offen lds\n\t"
-                 "buffer_load_dwordx4 %1, %3, %7 offen offset:1024 lds\n\t"
-                 "buffer_load_dwordx4 %0, %4, %7 offen offset:2048 lds\n\t"
-                 "buffer_load_dwordx4 %1, %5, %7 offen offset:3072 lds"
-                 :: "v"(voff0), "v"(voff1), "s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[3]), "s"(m0v), "s"(soff) : "memory", "m0");
-}
 
 // ------------------------------------------------------------------ decode (M <= 16)
 // Grid: T tiles x KS K-slices, one workgroup each, S waves per workgroup; wave w of slice k takes the groups
@@ -187,13 +39,8 @@ __device__ __forceinline__ void dma16_run4x(const __amdgpu_buffer_rsrc_t* r, uin
 // atomic exchange with 0, runs the epilogue and resets the counter, so part and cnt are zero again between calls.
 // No workgroup waits for another.  Atomics are coherent across the XCDs' L2s, so no cache write-back is needed.
 constexpr int DEC_MAXW = 16;
-#ifndef DEC_GPW_
-#define DEC_GPW_ 1
-#endif
-#ifndef DEC_MMA_MIN
-#define DEC_MMA_MIN 4
-#endif
-constexpr int DEC_GPW = DEC_GPW_;   // groups a wave keeps in flight at once
+constexpr int DEC_GPW = 1;         // groups a wave keeps in flight at once (2 to 4 measured slower)
+constexpr int DEC_MMA_MIN = 4;     // fewest tokens that take the matrix-core form
 
 // MP >= 4 runs the dot products on the matrix core: per 16 k-bytes one v_mfma_i32_32x32x32_i8 with the weights as
 // the B operand straight from the tile layout (lane l holds row l; column j of B is row j in the low k-half and row
@@ -381,26 +228,6 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
     }
 }
 
-// int64 -> fp32 (round to nearest even) for the epilogues: |v| < 2^52 is exact as a double (high word times 2^32
-// plus the low word, one fma), and the double -> float conversion then rounds once; larger magnitudes take
-// i64_to_f.
-__device__ __forceinline__ float i64_to_f_fast(long long v) {
-    const int hi = (int)(v >> 32);
-    if ((uint32_t)(hi + (1 << 20)) < (1u << 21)) {       // -2^52 <= v < 2^52
-        const double d = __builtin_fma((double)hi, 4294967296.0, (double)(uint32_t)v);
-        return (float)d;
-    }
-    return i64_to_f(v);
-}
-// start value of every MFMA chain in the biased scaling: |p| <= 128 * 127 * 128 < 2^21, so p + B >= 0
-constexpr uint32_t PF_BIAS = 1u << 21;
-// a * b for a, b < 2^16 (m and mx).  Inline asm: the compiler turns __umul24 of operands it cannot bound into an
-// AND and the quarter-rate v_mul_lo_u32.
-__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
-    uint32_t r;
-    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
 // ------------------------------------------------------------------ decode, many tokens (16 < M <= 64)
 // A workgroup of P (<= 4) wave pairs walks the groups g0 .. g1-1 of one tile's K-slice, pair p taking groups
 // g0 + p, g0 + p + P, ... (one round = one group per pair); wave h of a pair owns weight rows 32 h .. 32 h + 31 of the
@@ -421,15 +248,6 @@ __device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
 // `part`, counts itself in cnt[tile], and the last slice to arrive adds the other planes and writes the outputs.
 constexpr int DMS_MAXP = 4;          // wave pairs per workgroup
 constexpr int DMS_MAXSLOT = 96;      // groups per K-slice (digit slots in LDS)
-#if defined(DMS_TRACE)
-__device__ unsigned long long g_trace[4 * 64 * 8];
-#endif
-#ifdef DMS_TRACE
-#define DMS_TR(h, slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
-    __builtin_amdgcn_sched_barrier(0); if (blockIdx.x < 4 && threadIdx.x == 0 && (h) < 64) g_trace[(blockIdx.x * 64 + (h)) * 8 + (slot)] = tr_; } while (0)
-#else
-#define DMS_TR(h, slot) do {} while (0)
-#endif
 // bytes of v (slots s0 .. s0 + 3) at or past slot n set to zero
 __device__ __forceinline__ int mask_slots(int v, int s0, int n) {
     const int k = n - s0;
@@ -548,26 +366,19 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
     };
 
     int g = g0 + pr;
-    DMS_TR(62, 0);
     if (g < g1) fetch(g, area(0));
     for (int it = 0; it < rounds; it++, g += P) {
-        DMS_TR(it, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // this wave's copies and loads for round it have landed
-        DMS_TR(it, 1);
         __syncthreads();                                      // ... and the other waves' copies
-        DMS_TR(it, 2);
         uint32_t w[16];
 #pragma unroll
         for (int b = 0; b < 2; b++) block_signed<BITS>(q + b * NC, w + 8 * b);
         const uint32_t mr = m_n, mxl = mxl_n;
         if (g + P < g1) fetch(g + P, area((it + 1) & 1));   // the next round's loads run under this compute
-        DMS_TR(it, 3);
         if (g < g1) compute(area(it & 1), w, mr, mxl, g - g0);
-        DMS_TR(it, 4);
     }
     if (wv == 0 && lane < MT) sxs_s[lane] = sxl;
     __syncthreads();                                          // digits staged, activation areas free
-    DMS_TR(63, 0);
     // U -= B * S for block (row half hf, token set t) where t % P == pr:
     // S = sum_{i,j} 2^(7 (i + j)) D_ij, D_ij = sum over slots of digit i of mx times digit j of m
 #pragma unroll
@@ -606,7 +417,6 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
             }
         }
     }
-    DMS_TR(63, 1);
     // sums of the workgroup: tot[t][row], pair 0 writes, the others add
     long long* tot = reinterpret_cast<long long*>(xs_dyn);
     if (pr == 0) {
@@ -626,7 +436,6 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     __syncthreads();
-    DMS_TR(63, 2);
     // thread (wave w, lane) finishes tokens w + W i of row n (W = 2 or 4: at most MT / 2 of them), every load
     // before the first conversion, every conversion before the first store
     constexpr int EI = MT / 2;
@@ -687,351 +496,8 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
             if (t < mt) out.store(N, t0 + t, n, f[i]);
         }
     }
-    DMS_TR(63, 3);
 }
 
-// ------------------------------------------------------------------ prefill (M > 64)
-constexpr int P2_BM = 128;        // tokens per workgroup of k_prefill2
-
-// byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile
-// (chunk position c ^ ((r / 2) % 8): the 16 rows that one LDS cycle serves fall on 16 distinct 16-byte bank slots)
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
-
-#ifdef P2_TRACE
-__device__ unsigned long long g_trace2[4 * 4 * 64 * 8];
-#define P2_TR(it, slot) do { __builtin_amdgcn_sched_barrier(0); const unsigned long long tr_ = __builtin_amdgcn_s_memtime(); \
-    __builtin_amdgcn_sched_barrier(0); if (blockIdx.x < 4 && lane == 0 && (it) < 64) \
-    g_trace2[((blockIdx.x * 4 + wv) * 64 + (it)) * 8 + (slot)] = tr_; } while (0)
-#else
-#define P2_TR(it, slot) do {} while (0)
-#endif
-// ------------------------------------------------------------------ prefill, 128 x 64 tiles (M > 64)
-// Workgroup tile 128 tokens x 64 rows (one weight tile), 4 waves of 32 tokens x 64 rows; up to three workgroups per
-// CU (<= 168 VGPRs, <= 50 KB LDS), so a CU holds 12 waves whose MFMA chains, scaling and copy waits interleave.
-// Per 128-group g (one round):
-//   - every wave waits for its own copies and loads of round g and stages its multiplier; one barrier;
-//   - W4/W6: each lane unpacks its 32-code block of group g + 1 (wave = block, lane = row; the packed bytes were
-//     loaded into registers during the previous round) into the other half of the double-buffered signed tile Bs.
-//     W8 needs no unpack: the MFMA reads its B operand straight from a double-buffered copy of the codes (tile
-//     layout: plane c holds bytes 16 c .. 16 c + 15 of the 64 rows);
-//   - the activations of group g + 1 are copied by the buffer unit into LDS (W8 also its codes), the multipliers
-//     loaded into a register, W4/W6 group g + 2's packed block into registers;
-//   - 8 v_mfma_i32_32x32x32_i8 (two chains from the bias B) and the scaling U += (p + B) * (m * mx).
-// Group scaling with two VALU ops per (token, row, group): each group's MFMA chain starts from a constant
-// accumulator B = 2^21, so the int32 result p + B is never negative (|p| <= 128*127*128 < 2^21) and
-//     U += (p + B) * (m * mx)            (v_mul_u32_u24, v_mad_u64_u32; exact, U < 2^62)
-// The bias is removed once per output, acc = U - B * S with S = sum_g m[n,g] * mx[t,g], computed exactly on the
-// MFMA from unsigned 7-bit digits v = d0 + 128 d1 + 16384 d2 of m and mx, staged in LDS once per value:
-//     S = sum_{i,j} 2^(7 (i + j)) D_ij,   D_ij = sum_g dx_i[t,g] dw_j[n,g]   (every D_ij >= 0, no offset terms).
-template <int BITS>
-__global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__ wq, const float* __restrict__ cs,
-                                                      const uint16_t* __restrict__ ms, int N, int K,
-                                                      const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                      const uint16_t* __restrict__ mx, int M,
-                                                      Out out, int nbn, int nbt, int KS,
-                                                      long long* __restrict__ part, unsigned int* __restrict__ cnt) {
-    constexpr int NC = group_bytes(BITS) / 16;                 // 1 KB planes per tile-group
-    constexpr int WB = NC * 1024;
-    constexpr bool W8 = BITS == 8;    // W8: codes copied into a double-buffered staging tile the MFMA reads directly
-    __shared__ __attribute__((aligned(16))) int8_t As[2][P2_BM * 128];
-    __shared__ __attribute__((aligned(16))) int8_t Bp[2][W8 ? WB : 16];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[2][W8 ? 16 : TILE_N * 128];   // W4/W6: unpacked tiles
-    __shared__ __attribute__((aligned(16))) uint32_t mxs[2][P2_BM];   // mx of the tile's tokens, per buffer
-    __shared__ uint16_t mss[2][TILE_N];                                // m of the tile's rows, per buffer
-    __shared__ unsigned int last_s;
-
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wvu = __builtin_amdgcn_readfirstlane(wv);
-    const int l32 = lane & 31, lh = lane >> 5;
-    // XCD-aware order: consecutive workgroup ids go to different XCDs; each XCD gets a contiguous run of tiles,
-    // token blocks innermost, so the token blocks that share a weight tile (and K-slice) share an L2
-    int tile = blockIdx.x;
-    const int total = nbn * nbt * KS;
-    if ((total & 7) == 0) tile = (tile & 7) * (total >> 3) + (tile >> 3);
-    const int nb = tile / (nbt * KS), rem = tile - nb * (nbt * KS), ks = rem / nbt, tb = rem - ks * nbt;
-    const int t0 = tb * P2_BM, n0 = nb * TILE_N;
-    const int G = K / GROUP;
-    const int gs = (G + KS - 1) / KS;                          // groups of this workgroup's K-slice: [g0, g1)
-    const int g0 = ks * gs, g1 = min(G, g0 + gs);
-
-    unsigned long long U[2][16];
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) U[j][r] = 0;
-    v16i biasv;
-#pragma unroll
-    for (int r = 0; r < 16; r++) biasv[r] = (int)PF_BIAS;
-
-    // activations: copy i of wave wv takes rows t0 + 32 wv + 8 i + lane / 8 into As + 4096 wv + 1024 i, row R's chunk
-    // c at position c ^ ((R / 2) % 8); copy i reads through its own resource (based 8 i rows on, minus the 1 KB
-    // instruction offset) whose range ends at row M, so rows past M read as zero
-    __amdgpu_buffer_rsrc_t xr[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        xr[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(xq + (size_t)i * 8 * K - 1024 * i), (short)0,
-                                                  M > 8 * i ? (M - 8 * i) * K + 1024 * i : 0, 0x00020000);
-    const uint32_t a_vo = (uint32_t)(t0 + wv * 32 + (lane >> 3)) * (uint32_t)K + (uint32_t)(((lane & 7) ^ (lane >> 4)) * 16);
-    const uint32_t a_vo1 = a_vo ^ 64u;
-    // W8 codes: the tile-group is WB contiguous bytes; wave w copies planes 2 w, 2 w + 1
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)(wq + (size_t)nb * G * WB), (short)0, G * WB, 0x00020000);
-    const uint32_t w_vo[2] = {(uint32_t)lane * 16, (uint32_t)lane * 16};
-    // W4/W6 codes: wave w = block b (32 codes), lane = row r: bytes BPL b .. BPL b + BPL - 1 of the row's group,
-    // loaded into registers two groups ahead of their use (W4 plane b; W6 16 bytes of plane 3 (b / 2) + 2 (b % 2)
-    // and 8 bytes of plane 3 (b / 2) + 1 at byte 8 (b % 2), the odd blocks' low words starting with the latter)
-    const uint8_t* wcodes = wq + (size_t)nb * G * WB + lane * 16;
-    uint32_t qn[6];
-    auto load_w = [&](int g) __attribute__((always_inline)) {
-        const uint8_t* p = wcodes + (size_t)g * WB;
-        if constexpr (BITS == 4) {
-            const uint4 v = *reinterpret_cast<const uint4*>(p + wvu * 1024);
-            qn[0] = v.x; qn[1] = v.y; qn[2] = v.z; qn[3] = v.w;
-        } else if constexpr (BITS == 6) {
-            const int pp = 3 * (wvu >> 1);
-            const uint4 v = *reinterpret_cast<const uint4*>(p + (pp + 2 * (wvu & 1)) * 1024);
-            const uint2 w = *reinterpret_cast<const uint2*>(p + (pp + 1) * 1024 + 8 * (wvu & 1));
-            qn[0] = v.x; qn[1] = v.y; qn[2] = v.z; qn[3] = v.w; qn[4] = w.x; qn[5] = w.y;
-        }
-    };
-    // unpack the registers' block into the signed tile bs (row lane, chunks 2 b and 2 b + 1); the W6 reorder of odd
-    // blocks happens here, not at the load, so no wait for the load is placed early
-    auto unpack_to = [&](int8_t* bs) __attribute__((always_inline)) {
-        uint32_t o[8];
-        if constexpr (BITS == 6) {
-            const bool odd = wvu & 1;
-            const uint32_t w6[6] = {odd ? qn[4] : qn[0], odd ? qn[5] : qn[1], odd ? qn[0] : qn[2],
-                                    odd ? qn[1] : qn[3], odd ? qn[2] : qn[4], odd ? qn[3] : qn[5]};
-            block_signed<6>(w6, o);
-        } else {
-            block_signed<W8 ? 4 : BITS>(qn, o);
-        }
-        *reinterpret_cast<uint4*>(bs + swz(lane, 2 * wvu)) = make_uint4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<uint4*>(bs + swz(lane, 2 * wvu + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
-    };
-    // multipliers: thread tid < 128 loads mx[t0 + tid][g] (1 for tokens past M or without mx), 128 <= tid < 192
-    // m[tile][g][tid - 128], by plain zero-extending loads (a 16-bit buffer load's result needs a mask, for which
-    // the compiler can wait at once)
-    const bool xm = tid < P2_BM, wm_ = tid >= P2_BM && tid < P2_BM + TILE_N;
-    const bool x_one = xm && !(mx && t0 + tid < M);
-    const bool s_load = (xm && !x_one) || wm_;
-    const uint16_t* s_ptr = xm ? (x_one ? ms : mx + (size_t)(t0 + tid) * G) : ms + (size_t)nb * G * 64 + (wm_ ? tid - P2_BM : 0);
-    const int s_stride = xm ? 1 : 64;
-    uint32_t sreg = 1;
-
-    auto issue_a = [&](int g) __attribute__((always_inline)) {
-        dma16_run4x(xr, a_vo, a_vo1, g * GROUP, As[g & 1] + wvu * 4096);
-    };
-    auto issue_s = [&](int g) __attribute__((always_inline)) {
-        if (s_load) sreg = s_ptr[(size_t)g * s_stride];
-    };
-
-    P2_TR(63, 0);
-    issue_a(g0);
-    issue_s(g0);
-    if constexpr (W8) {
-        dma16_run<2>(wr, w_vo, g0 * WB + wvu * 2048, Bp[g0 & 1] + wvu * 2048);
-    } else {
-        load_w(g0);
-        unpack_to(Bs[g0 & 1]);
-        if (g0 + 1 < g1) load_w(g0 + 1);
-    }
-    for (int g = g0; g < g1; g++) {
-        const int par = g & 1;
-        P2_TR(g, 0);
-        asm volatile("s_waitcnt vmcnt(0)" : "+v"(sreg) :: "memory");
-        P2_TR(g, 1);
-        if (xm) mxs[par][tid] = x_one ? 1u : sreg;
-        else if (wm_) mss[par][tid - P2_BM] = (uint16_t)sreg;
-        __syncthreads();                      // group g's copies and unpacked codes are in place; group g - 1's
-                                              // compute is done, so the other buffers are free
-        P2_TR(g, 2);
-        if constexpr (!W8) {
-            // group g + 1's codes (loaded during the previous round) into the other tile, before any new load is
-            // issued (so the wait for those registers finds nothing newer outstanding)
-            if (g + 1 < g1) unpack_to(Bs[(g + 1) & 1]);
-        }
-        P2_TR(g, 3);
-        if (g + 1 < g1) {
-            issue_a(g + 1);
-            issue_s(g + 1);
-            if constexpr (W8) dma16_run<2>(wr, w_vo, (g + 1) * WB + wvu * 2048, Bp[(g + 1) & 1] + wvu * 2048);
-            else if (g + 2 < g1) load_w(g + 2);
-        }
-        P2_TR(g, 4);
-        // MFMA over group g and scaling into U
-        const int8_t* Ab = As[par];
-        v16i d[2];
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const v4i a = *reinterpret_cast<const v4i*>(Ab + swz(wv * 32 + l32, 2 * s + lh));
-            v4i b0, b1;
-            if constexpr (BITS == 8) {
-                const int8_t* Bb = Bp[par] + (2 * s + lh) * 1024;
-                b0 = *reinterpret_cast<const v4i*>(Bb + l32 * 16);
-                b1 = *reinterpret_cast<const v4i*>(Bb + (32 + l32) * 16);
-            } else {
-                b0 = *reinterpret_cast<const v4i*>(Bs[par] + swz(l32, 2 * s + lh));
-                b1 = *reinterpret_cast<const v4i*>(Bs[par] + swz(32 + l32, 2 * s + lh));
-            }
-            d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, s == 0 ? biasv : d[0], 0, 0, 0);
-            d[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, s == 0 ? biasv : d[1], 0, 0, 0);
-        }
-        // element (t, n): lane n % 32 + 32 ((t / 4) % 2), register 4 (t / 8) + t % 4 of chain n / 32
-        const uint32_t m0 = mss[par][l32], m1 = mss[par][32 + l32];
-#pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            const uint4 mv = *reinterpret_cast<const uint4*>(&mxs[par][wv * 32 + 8 * q4 + 4 * lh]);
-            const uint32_t mxv[4] = {mv.x, mv.y, mv.z, mv.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                U[0][4 * q4 + e] += (unsigned long long)(uint32_t)d[0][4 * q4 + e] * mul_u24(m0, mxv[e]);
-                U[1][4 * q4 + e] += (unsigned long long)(uint32_t)d[1][4 * q4 + e] * mul_u24(m1, mxv[e]);
-            }
-        }
-    }
-
-    P2_TR(63, 1);
-    // ---- bias correction: S = sum_g m * mx from 7-bit digits on the MFMA, 32 groups at a time, staged in As:
-    // xd[i][t][32] of mx (128 tokens), wd[i][n][32] of m (64 rows)
-    __syncthreads();                          // every wave is done with As
-    int8_t* xd = As[0];                       // [3][128][32] = 12 KB
-    int8_t* wd = As[1];                       // [3][64][32] = 6 KB
-    float* sxs = reinterpret_cast<float*>(As[1] + 8192);
-    if (tid < P2_BM) sxs[tid] = sx[min(t0 + tid, M - 1)];
-    // thread tid stages 16 groups of token tid / 2 (half tid % 2); threads < 128 also 16 groups of row tid / 2
-    const int sl = tid >> 1, sh = (tid & 1) * 16;
-    const bool tok_ok = mx && t0 + sl < M;
-    const uint16_t* mrow = mx + (size_t)(t0 + sl) * G;
-    const uint16_t* wrow = ms + (size_t)nb * G * 64 + (sl & 63);
-    auto digits4 = [](const uint32_t* v, uint32_t& w0, uint32_t& w1, uint32_t& w2) __attribute__((always_inline)) {
-        const uint32_t p01 = v[0] | (v[1] << 16), p23 = v[2] | (v[3] << 16);
-        w0 = __builtin_amdgcn_perm(p23 & 0x007f007fu, p01 & 0x007f007fu, 0x06040200u);
-        w1 = __builtin_amdgcn_perm((p23 >> 7) & 0x007f007fu, (p01 >> 7) & 0x007f007fu, 0x06040200u);
-        w2 = __builtin_amdgcn_perm((p23 >> 14) & 0x00030003u, (p01 >> 14) & 0x00030003u, 0x06040200u);
-    };
-    for (int k0 = g0; k0 < g1; k0 += 32) {
-        uint32_t xv[16], wv_[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int g = k0 + sh + e;
-            xv[e] = g < g1 ? (tok_ok ? (uint32_t)mrow[g] : 1u) : 0u;
-            wv_[e] = g < g1 && tid < 2 * TILE_N ? (uint32_t)wrow[(size_t)g * 64] : 0u;
-        }
-        uint32_t xw[3][4], ww[3][4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            digits4(xv + 4 * q, xw[0][q], xw[1][q], xw[2][q]);
-            digits4(wv_ + 4 * q, ww[0][q], ww[1][q], ww[2][q]);
-        }
-        if (k0 > g0) __syncthreads();         // the previous chunk's digit reads are done
-#pragma unroll
-        for (int d = 0; d < 3; d++) {
-            *reinterpret_cast<uint4*>(xd + (d * P2_BM + sl) * 32 + sh) = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
-            if (tid < 2 * TILE_N)
-                *reinterpret_cast<uint4*>(wd + (d * TILE_N + sl) * 32 + sh) = make_uint4(ww[d][0], ww[d][1], ww[d][2], ww[d][3]);
-        }
-        __syncthreads();
-        v4i A[3];
-#pragma unroll
-        for (int d = 0; d < 3; d++) A[d] = *reinterpret_cast<const v4i*>(xd + (d * P2_BM + wv * 32 + l32) * 32 + 16 * lh);
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            v4i Bd[3];
-#pragma unroll
-            for (int d = 0; d < 3; d++) Bd[d] = *reinterpret_cast<const v4i*>(wd + (d * TILE_N + j * 32 + l32) * 32 + 16 * lh);
-            const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-            // digit weights 2^28 (sum < 2^9), 2^21 (< 2^15), 2^14 (< 2^21), 2^7 (< 2^20): t stays below 2^32
-            v16i t = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[2], z, 0, 0, 0);
-            v16i e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[1], z, 0, 0, 0);
-            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[2], e, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
-            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[2], Bd[0], z, 0, 0, 0);
-            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[1], e, 0, 0, 0);
-            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[2], e, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
-            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1], Bd[0], z, 0, 0, 0);
-            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[1], e, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; r++) t[r] = (int)(((uint32_t)t[r] << 7) + (uint32_t)e[r]);
-            e = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], Bd[0], z, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const unsigned long long S = ((unsigned long long)(uint32_t)t[r] << 7) + (uint32_t)e[r];
-                U[j][r] -= S << 21;
-            }
-        }
-    }
-
-    P2_TR(63, 2);
-    // ---- K-slices: every slice stores its exact int64 sums into its own plane of `part` (agent-scope stores,
-    // coherent across the XCDs' L2s), waits until they are performed and counts itself in cnt[tile]; the slice
-    // that arrives last adds the other planes and runs the epilogue, then resets the counter
-    if (KS > 1) {
-        const size_t npad = (size_t)nbn * TILE_N, mpad = (size_t)nbt * P2_BM;
-        const int tcount = tb * nbn + nb;
-        const int tr0 = t0 + wv * 32 + 4 * lh;                   // token of register 0; register r adds 8 (r / 4) + r % 4
-        auto at = [&](int k, int j, int r) __attribute__((always_inline)) {
-            return part + ((size_t)k * mpad + tr0 + 8 * (r >> 2) + (r & 3)) * npad + n0 + 32 * j + l32;
-        };
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-                __hip_atomic_store(at(ks, j, r), (long long)U[j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);             // this wave's stores have been performed
-        __syncthreads();
-        if (tid == 0)
-            last_s = __hip_atomic_fetch_add(cnt + tcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);
-        __syncthreads();
-        if (!last_s) return;
-        for (int k = 0; k < KS; k++) {
-            if (k == ks) continue;
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++)
-                    U[j][r] += (unsigned long long)__hip_atomic_load(at(k, j, r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (tid == 0) __hip_atomic_store(cnt + tcount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // ---- epilogue: y = (f32(acc) * c[n]) * sx[t]; a tile routed whole to one plain output stores unchecked
-    const bool full = t0 + P2_BM <= M && n0 + TILE_N <= N && out.nparts <= 1;
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int n = n0 + 32 * j + l32;
-        const float cn = n < N ? cs[n] : 0.0f;
-        float v[16];
-#pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            const float4 sv = *reinterpret_cast<const float4*>(sxs + wv * 32 + 8 * q4 + 4 * lh);
-            const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) v[4 * q4 + e] = (i64_to_f_fast((long long)U[j][4 * q4 + e]) * cn) * svv[e];
-        }
-        const int tb = t0 + wv * 32 + 4 * lh;        // token of register 0; register r adds 8 (r / 4) + r % 4
-        if (full) {
-            float* yb = out.y + (size_t)tb * N + n;
-            if (out.acc) {
-                float old[16];
-#pragma unroll
-                for (int r = 0; r < 16; r++) old[r] = yb[(size_t)(8 * (r >> 2) + (r & 3)) * N];
-#pragma unroll
-                for (int r = 0; r < 16; r++) v[r] = old[r] + v[r];
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) yb[(size_t)(8 * (r >> 2) + (r & 3)) * N] = v[r];
-        } else {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int t = tb + 8 * (r >> 2) + (r & 3);
-                if (t < M && n < N) out.store(N, t, n, v[r]);
-            }
-        }
-    }
-    P2_TR(63, 3);
-}
 
 // ------------------------------------------------------------------ load-time repack and quantizer
 __global__ void k_repack(const uint8_t* __restrict__ rows, int N, int K, int bits, uint8_t* __restrict__ wq,
@@ -1266,24 +732,12 @@ void gemm_bits(const det_qlinear& L, const int8_t* xq, const float* sx, const ui
         const bool split = M > 32 && 2 * T * dms_slices(2 * T, G) > T * dms_slices(T, G);
         if (M <= 32 || split) launch_decode_ms<BITS, 1>(L, xq, sx, mx, M, y, st);
         else launch_decode_ms<BITS, 2>(L, xq, sx, mx, M, y, st);
-    } else {
-        const int nbn = (L.N + TILE_N - 1) / TILE_N, nbt = (M + P2_BM - 1) / P2_BM;
-        // K-slices when the tiles leave CUs idle: up to 1.5 workgroups per CU, each slice at least 16 groups (the
-        // combine costs about as much as a few groups)
-        const int G = L.K / GROUP, tiles = nbn * nbt, cus = g_decode_waves / 8;
-        int KS = 1;
-        if (2 * tiles < 3 * cus) KS = std::max(1, std::min((3 * cus + 2 * tiles - 1) / (2 * tiles), G / 16));
-        const int gs = (G + KS - 1) / KS;
-        KS = (G + gs - 1) / gs;                  // no empty slices
-        long long* part = nullptr;
-        unsigned int* cnt = nullptr;
-        if (KS > 1) {
-            part = partial_buffer((size_t)KS * nbt * P2_BM * nbn * TILE_N, st);
-            decode_buffers(0, (size_t)tiles, st);
-            cnt = g_cnt;
-        }
-        k_prefill2<BITS><<<tiles * KS, 256, 0, st>>>(L.wq, L.c, L.m, L.N, L.K, xq, sx, mx, M, y, nbn, nbt, KS, part, cnt);
-        DET_CHECK(hipGetLastError());
+    } else if (!prefill_gemm(L, xq, sx, mx, M, y, g_decode_waves / 8, st)) {
+        // shapes outside the prefill kernel (K >= 131072 or M * K >= 2^31): 16-token slices of the decode kernel
+        const int G = L.K / GROUP;
+        for (int t = 0; t < M; t += 16)
+            launch_decode<BITS, 16>(L, xq + (size_t)t * L.K, sx + t, mx ? mx + (size_t)t * G : nullptr, std::min(16, M - t),
+                                    y.rows_from(L.N, t), st);
     }
 }
 
@@ -1296,18 +750,21 @@ void det_linear_sizes(int N, int K, int bits, size_t* wq_bytes, size_t* c_bytes,
     if (bits != 4 && bits != 6 && bits != 8) DET_FAIL("det_linear_sizes: unsupported bits=%d", bits);
     // whole 128-row blocks (pairs of 64-row tiles): the prefill kernel reads weight tiles two at a time
     const size_t T = 2 * (((size_t)N + 2 * TILE_N - 1) / (2 * TILE_N)), G = (size_t)K / GROUP;
-    if (wq_bytes) *wq_bytes = T * G * group_bytes(bits) * TILE_N;
+    // the decode tiles, then the prefill planes (the same size: 32-row blocks of the same row pairs)
+    if (wq_bytes) *wq_bytes = 2 * T * G * group_bytes(bits) * TILE_N;
     if (c_bytes) *c_bytes = T * TILE_N * 4;
     if (m_bytes) *m_bytes = T * G * TILE_N * 2;
 }
 
 void det_linear_repack(const uint8_t* rows, int N, int K, int bits, uint8_t* wq, float* c, uint16_t* m, hipStream_t st) {
-    size_t wb;
-    det_linear_sizes(N, K, bits, &wb, nullptr, nullptr);
-    const size_t nchunks = wb / 16;
+    det_linear_sizes(N, K, bits, nullptr, nullptr, nullptr);     // validates the shape
+    // the decode tiles only: k_repack also writes c and m for every tile it visits, and those planes cover the
+    // decode tiles (the prefill planes that follow in wq are written by prefill_repack)
+    const size_t nchunks = pf_offset(N, K, bits) / 16;
     const size_t blocks = std::min<size_t>((nchunks + 255) / 256, 65536);
     k_repack<<<(unsigned)blocks, 256, 0, st>>>(rows, N, K, bits, wq, c, m, nchunks);
     DET_CHECK(hipGetLastError());
+    prefill_repack(rows, N, K, bits, wq, st);
 }
 
 void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hipStream_t st) {
@@ -1318,18 +775,6 @@ void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hi
     DET_CHECK(hipGetLastError());
 }
 
-#if defined(P2_TRACE)
-void det_debug_trace2(unsigned long long* host) {
-    DET_CHECK(hipDeviceSynchronize());
-    DET_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace2), sizeof(g_trace2)));
-}
-#endif
-#if defined(DMS_TRACE)
-void det_debug_trace(unsigned long long* host) {
-    DET_CHECK(hipDeviceSynchronize());
-    DET_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace)));
-}
-#endif
 size_t det_gemm_scratch_bytes(int M, int K) { return (size_t)(M < 1 ? 1 : M) * (size_t)((K + 127) / 128) * sizeof(int); }
 void det_gemm_set_scratch(void* p, size_t bytes) { g_user_scratch = p; g_user_scratch_bytes = p ? bytes : 0; }
 

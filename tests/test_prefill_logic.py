@@ -1,0 +1,181 @@
+"""CPU checks of the prefill kernel's host-independent logic (det_amd/csrc/prefill.hip), restated here:
+
+* the prefill-plane packing of k_repack_pf and the kernel's unpack (pf_unpack) are inverse: every signed code of
+  every width comes back scaled by 2^SH, at the k the MFMA step expects;
+* the stream-K split: the workgroup ranges partition the units, pf_owner names the workgroup of every unit, the
+  partial-tile slots of split fragments are distinct and inside the 2 P slots the host allocates, the arrival count
+  that marks the last fragment equals the tile's fragment count, and the host's no-split test is exact;
+* every memory access of k_prefill and k_repack_pf stays inside its allocation (buffer-unit rule: per-lane offset
+  plus instruction offset checked against the resource size, scalar offset unchecked), over shapes with partial
+  token and row tiles.
+A change to that arithmetic in prefill.hip must be made here too.
+"""
+import itertools
+
+import numpy as np
+import pytest
+
+from tests.test_kernel_bounds import reached, check_in
+from tests.test_quantizer_parity import pf_unpack
+
+GROUP = 128
+NP = {8: 4, 6: 3, 4: 2}
+SH = {8: 0, 6: 2, 4: 4}
+
+
+def pack_lane(c, bits):
+    """k_repack_pf: one lane's 64 codes (k order of the lane) -> 4 NP words."""
+    q = []
+    for s in range(4):
+        cs = c[16 * s:16 * s + 16]
+        if bits == 8:
+            for d in range(4):
+                q.append(sum((int(cs[4 * d + j]) & 255) << (8 * j) for j in range(4)))
+        elif bits == 6:
+            for i in range(3):
+                q.append(sum((((int(cs[4 * i + j]) & 63) << 2) | ((int(cs[12 + j]) >> (4 - 2 * i)) & 3)) << (8 * j)
+                             for j in range(4)))
+        else:
+            for i in range(2):
+                q.append(sum((((int(cs[8 * i + j]) & 15) << 4) | (int(cs[8 * i + 4 + j]) & 15)) << (8 * j)
+                             for j in range(4)))
+    return np.array(q, np.uint32)
+
+
+@pytest.mark.parametrize('bits', [4, 6, 8])
+def test_pack_unpack_inverse(bits):
+    qmax = (1 << (bits - 1)) - 1
+    lo = -qmax - 1
+    rng = np.random.default_rng(bits)
+    cases = [np.arange(64) % (qmax - lo + 1) + lo, np.full(64, lo), np.full(64, qmax), np.zeros(64, np.int64)]
+    cases += [rng.integers(lo, qmax + 1, 64) for _ in range(200)]
+    for c in cases:
+        got = pf_unpack(pack_lane(c, bits), bits)
+        assert (got == np.asarray(c, np.int64) << SH[bits]).all()
+        assert np.abs(got).max() <= 128
+    # |p| bound of the scaled codes: 128 * 127 * 128 < 2^21 at every width
+    assert 128 * 127 * (qmax + 1) << SH[bits] <= 128 * 127 * 128 < 1 << 21
+
+
+def owner(u, total, P):
+    return ((u + 1) * P + total - 1) // total - 1
+
+
+def ranges(total, P):
+    return [(w * total // P, (w + 1) * total // P) for w in range(P)]
+
+
+def host_P(total, cus):
+    P = min(2 * cus, max(1, total // 4))
+    if P > 8:
+        P &= ~7
+    return P
+
+
+def fragments(tiles, G, P):
+    total = tiles * G
+    out = []
+    for w, (u0, u1) in enumerate(ranges(total, P)):
+        u = u0
+        while u < u1:
+            tile = u // G
+            ga = u - tile * G
+            gb = min(G, u1 - tile * G)
+            out.append((w, tile, ga, gb))
+            u = tile * G + gb
+    return out
+
+
+@pytest.mark.parametrize('tiles,G', [(304, 20), (1, 20), (3, 1), (7760, 20), (80, 32), (40, 136), (76, 76), (2, 2),
+                                     (5, 48), (160, 80), (8, 8)])
+@pytest.mark.parametrize('cus', [256, 80, 4])
+def test_stream_k_bookkeeping(tiles, G, cus):
+    total = tiles * G
+    P = host_P(total, cus)
+    fr = fragments(tiles, G, P)
+    # the ranges partition the units in order; fragments partition each tile's groups
+    seen = np.zeros(total, np.int64)
+    for w, tile, ga, gb in fr:
+        assert 0 <= ga < gb <= G
+        seen[tile * G + ga:tile * G + gb] += 1
+        for u in (tile * G + ga, tile * G + gb - 1):
+            assert owner(u, total, P) == w
+    assert (seen == 1).all()
+    split = total % P != 0 or (total // P) % G != 0
+    slots = set()
+    for w, tile, ga, gb in fr:
+        whole = ga == 0 and gb == G
+        if not whole:
+            assert split, 'a split fragment without the partial buffer'
+            wf, wl = owner(tile * G, total, P), owner(tile * G + G - 1, total, P)
+            assert wf <= w <= wl
+            nfrag = sum(1 for f in fr if f[1] == tile)
+            assert nfrag == wl - wf + 1
+            first_tile = (w * total // P) // G
+            slot = 2 * w + (0 if first_tile == tile else 1)
+            assert slot not in slots and 0 <= slot < 2 * P
+            slots.add(slot)
+    # a workgroup has at most two split fragments (its first and its last)
+    for w in range(P):
+        mine = [f for f in fr if f[0] == w and not (f[2] == 0 and f[3] == G)]
+        assert len(mine) <= 2
+
+
+def prefill_accesses(N, K, M, bits, cus=256):
+    G = K // GROUP
+    nbn, nbt = (N + 127) // 128, (M + 127) // 128
+    tiles = nbn * nbt
+    total = tiles * G
+    P = host_P(total, cus)
+    np_ = NP[bits]
+    T64 = 2 * nbn
+    pf_size = T64 * G * 64 * 4 * {8: 32, 6: 24, 4: 16}[bits]      # the prefill planes
+    m_size, mx_size, x_size = T64 * G * 64 * 2, M * G * 2, M * K
+    lane = np.arange(64)
+    for w, tile, ga, gb in fragments(tiles, G, P):
+        nb, tb = divmod(tile, nbt)
+        t0, n0 = tb * 128, nb * 128
+        for g in sorted({ga, (ga + gb) // 2, gb - 1}):
+            for wv in range(4):
+                # activations: one resource of M K bytes; copy i at avo[i] + 1024 i, scalar offset 128 g
+                for i in range(4):
+                    row = t0 + wv * 32 + 8 * i + (lane >> 3)
+                    avo = row * K - 1024 * i + (((lane & 7) ^ (((i & 1) << 2) | (lane >> 4))) * 16)
+                    assert (avo >= 0).all()
+                    lo, hi = reached(0, avo, 1024 * i, GROUP * g, x_size)
+                    check_in(lo, hi, x_size, f'prefill A copy N={N} K={K} M={M}')
+                    # the chunk a lane lands must be chunk (p ^ ((R/2) % 8)) of its token row R
+                    R = wv * 32 + 8 * i + (lane >> 3)
+                    p = lane & 7
+                    assert ((avo + 1024 * i - row * K) // 16 == (p ^ ((R >> 1) & 7))).all()
+                    assert 4096 * wv + 1024 * i + 16 * lane.max() + 16 <= 128 * 128
+                # codes: block resource of G NP 1 KB at (nb 4 + wv) G NP 1 KB, per-lane 16 lane, offsets 1 KB p
+                blk = nb * 4 + wv
+                for pl in range(np_):
+                    lo, hi = reached(blk * G * np_ * 1024, lane * 16, 1024 * pl, g * np_ * 1024, G * np_ * 1024)
+                    check_in(lo, hi, pf_size, 'prefill code load')
+                    assert (lo >= blk * G * np_ * 1024).all() and (hi <= (blk + 1) * G * np_ * 1024).all()
+                # multipliers: waves 0-1 m of row n0 + sidx, waves 2-3 mx of token t0 + sidx
+                sidx = (64 * wv + lane) & 127
+                if wv < 2:
+                    n = n0 + sidx
+                    vo = ((n >> 6) * G * 64 + (n & 63)) * 2 + 128 * g
+                    lo, hi = reached(0, vo, 0, 0, nbn * 2 * G * 128, 2)
+                    check_in(lo, hi, m_size, 'prefill m load')
+                    assert len(lo) == 64
+                else:
+                    vo = (t0 + sidx) * G * 2 + 2 * g
+                    lo, hi = reached(0, vo, 0, 0, mx_size, 2)
+                    check_in(lo, hi, mx_size, 'prefill mx load')
+                    assert len(lo) == int(((t0 + sidx) < M).sum())
+
+
+SHAPES = [(640, 2560), (9728, 2560), (2560, 9728), (200, 384), (48, 128), (17408, 5120), (5120, 17408), (64, 2560),
+          (10240, 2560)]
+
+
+@pytest.mark.parametrize('bits', [4, 6, 8])
+@pytest.mark.parametrize('N,K', SHAPES)
+def test_prefill_accesses_in_bounds(N, K, bits):
+    for M in (65, 100, 128, 300, 512):
+        prefill_accesses(N, K, M, bits)
