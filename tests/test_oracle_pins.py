@@ -305,3 +305,142 @@ def test_treesum_order():
     assert np.float32(L.ora_treesum(v.ctypes.data, v.size)) == want
     ints = np.arange(1, 1001, dtype=np.float32)                   # exact integer sums are order-free
     assert L.ora_treesum(ints.ctypes.data, ints.size) == 500500.0
+
+
+# ---------------------------------------------------------------- the quantizer's scale search (quantize.rs:33-55)
+# A one-group row (K = 128) keeps its chosen scale s in the row: m = 65535 and c = f32(s / 65535), so s is read
+# back to within 2^-23 relative, and the step follows from s / base = 0.80 + 0.02 step (steps 2 % apart).
+def chosen_step(w, bits):
+    qmax = (1 << (bits - 1)) - 1
+    row = oracle.quantize_rows(np.asarray(w, np.float32).reshape(1, 128), bits)[0]
+    nc = 4 * {8: 32, 6: 24, 4: 16}[bits]
+    c = float(row[nc:nc + 4].view('<f4')[0])
+    assert row[nc + 4:].view('<u2')[0] == 65535
+    base = float(np.abs(np.asarray(w, np.float64)).max()) / qmax
+    r = (c * 65535.0 / base - 0.80) / 0.02
+    step = int(round(r))
+    assert abs(r - step) < 1e-3, r
+    return step
+
+
+def exact_sse(w, bits, step):
+    """The squared error of candidate `step` in exact rational arithmetic (no float rounding anywhere)."""
+    qmax = (1 << (bits - 1)) - 1
+    wv = [Fraction(float(v)) for v in np.asarray(w, np.float32)]
+    base = max(abs(v) for v in wv) / qmax
+    s = base * (Fraction(4, 5) + Fraction(step, 50))
+    err = Fraction(0)
+    for v in wv:
+        x = v / s
+        q = round(x)                       # Python rounds halves to even, as round_ties_even
+        q = max(-qmax, min(qmax, q))
+        err += (q * s - v) ** 2
+    return err
+
+
+def brute_step(w, bits):
+    """The first candidate of least exact error, and the margin to the runner-up (relative)."""
+    errs = [exact_sse(w, bits, k) for k in range(11)]
+    best = min(range(11), key=lambda k: (errs[k], k))
+    others = [e for k, e in enumerate(errs) if k != best]
+    return best, float((min(others) - errs[best]) / max(min(others), Fraction(1, 10 ** 30)))
+
+
+def test_scale_search_step10_exact_grid():
+    """Every value an integer multiple of base (a power of two): step 10 has zero error and every other step clamps
+    amax, so step 10 is the unique best; a loop that stops at step 9 fails."""
+    for bits in (4, 6, 8):
+        qmax = (1 << (bits - 1)) - 1
+        b = 2.0 ** -9
+        j = (np.arange(128) * 37) % (2 * qmax + 1) - qmax
+        j[5] = qmax
+        w = (j * b).astype(np.float32)
+        assert brute_step(w, bits)[0] == 10
+        assert chosen_step(w, bits) == 10
+
+
+def test_scale_search_every_step():
+    """For each candidate k: amax = qmax * base and the other values on the grid of s_k (multiples j s_k that stay
+    unclamped), drawn with a preference for multiples far from the other candidates' grids.  Step k then has the
+    amax term as its only error; the first seeded draw whose exact brute-force winner is k by a clear margin is kept,
+    and the oracle must pick k for it.  With one clamped amax the small steps can only win at W4 (the amax error
+    (qmax (0.2 - 0.02 k) base)^2 outgrows what 127 grid values can cost the other steps): W4 isolates all 11 steps,
+    W6 steps 5-10, W8 steps 9-10.  That fixes the first candidate (0.80), the increment (0.02) and the count (11): a
+    wrong start, increment or range picks another scale."""
+    rng = np.random.default_rng(1)
+    reach = {4: range(0, 11), 6: range(5, 11), 8: range(9, 11)}
+    for bits in (4, 6, 8):
+        qmax = (1 << (bits - 1)) - 1
+        for k in reach[bits]:
+            base = 2.0 ** -8
+            s = base * (0.80 + 0.02 * k)
+            lim = min(qmax, int(qmax * base / s))      # multiples that stay unclamped at s_k
+            cand = np.arange(1, lim + 1)
+            v = cand * (0.80 + 0.02 * k)
+            far = sum((np.abs(v / sm - np.round(v / sm)) * sm) ** 2
+                      for sm in (0.80 + 0.02 * m for m in range(11) if m != k))
+            for _ in range(300):
+                p = np.exp(far * rng.uniform(1, 40))
+                j = rng.choice(cand, 128, p=p / p.sum()) * rng.choice([-1, 1], 128)
+                w = (j * s).astype(np.float32)
+                w[7] = np.float32(qmax * base)
+                best, margin = brute_step(w, bits)
+                if best == k and margin > 0.01:
+                    break
+            else:
+                raise AssertionError(f'no isolating group for W{bits} step {k}')
+            assert chosen_step(w, bits) == k, (bits, k)
+
+
+def test_scale_search_random_groups_against_exact_brute_force():
+    """Gaussian groups: whenever the exact brute force has a winner by a margin well above f64 rounding, the oracle
+    picks it."""
+    rng = np.random.default_rng(4)
+    checked = 0
+    for bits in (4, 6, 8):
+        for _ in range(40):
+            w = (rng.standard_normal(128) * 0.02).astype(np.float32)
+            best, margin = brute_step(w, bits)
+            if margin < 1e-9:
+                continue
+            assert chosen_step(w, bits) == best
+            checked += 1
+    assert checked > 100
+
+
+def test_scale_search_zero_group():
+    """An all-zero group takes scale 1.0 (quantize.rs:35-37): c = f32(1 / 65535), m = 65535, codes 0."""
+    for bits in (4, 6, 8):
+        row = oracle.quantize_rows(np.zeros((1, 128), np.float32), bits)[0]
+        nc = 4 * {8: 32, 6: 24, 4: 16}[bits]
+        assert row[nc:nc + 4].view('<f4')[0] == np.float32(1.0 / 65535.0)
+        assert row[nc + 4:].view('<u2')[0] == 65535
+        assert (oracle.unpack_row(row[:nc], bits, 128) == 0).all()
+
+
+def test_quant_act_multiplies_by_the_reciprocal():
+    """quant_act_i8g (spec/quant.rs:21-49) scales by inv = 1 / (sx * mx), a multiply, not a division: values where
+    rint(x * f32(1 / eff)) and rint(x / eff) differ follow the multiply.  The row has one group whose max sets
+    sx = amax / 127 / 65535 and mx = 65535."""
+    rng = np.random.default_rng(8)
+    found = 0
+    for _ in range(2000):
+        amax = np.float32(rng.uniform(0.5, 2.0))
+        sg = np.float32(amax / np.float32(127.0))
+        sx = np.float32(sg / np.float32(65535.0))
+        eff = np.float32(sx * np.float32(65535.0))
+        inv = np.float32(np.float32(1.0) / eff)
+        # candidates just around the rounding midpoints j + 1/2
+        x = np.float32((rng.integers(0, 127) + 0.5) * float(eff))
+        for cand in (x, np.nextafter(x, np.float32(0)), np.nextafter(x, np.float32(10))):
+            a = np.rint(np.float32(cand * inv))
+            b = np.rint(np.float32(cand / eff))
+            if a != b and abs(cand) < amax:
+                row = np.zeros((1, 128), np.float32)
+                row[0, 0] = amax
+                row[0, 1] = cand
+                xq, sxo, mxo = oracle.quant(row)
+                assert sxo[0] == sx and mxo[0, 0] == 65535
+                assert xq[0, 1] == int(a), (cand, a, b)
+                found += 1
+    assert found >= 3, found
