@@ -30,7 +30,10 @@ def P(a):
 class OracleModel:
     """qwen35::forward (qwen35.rs:8-172) and Model::forward / embed_rows (model.rs:390-466) over the oracle."""
 
-    def __init__(self, data):
+    def __init__(self, data, ctx=CTX, fast=False):
+        """data: the det GGUF's bytes.  fast: the GEMMs on det's x86 GEMM restated in C (oracle/x86_gemm.c, pinned
+        bit for bit to the scalar oracle) instead of the scalar oracle."""
+        self.ctx, self.fast, self.x86 = ctx, fast, {}
         kv, self.t = R.read_gguf(data)
         a = lambda k: kv['qwen35.' + k][1]
         self.h, self.ff = a('embedding_length'), a('feed_forward_length')
@@ -48,8 +51,8 @@ class OracleModel:
 
     def reset(self):
         self.pos = 0
-        self.kv = [(np.zeros((CTX, self.n_kv, self.hd), np.int8), np.zeros((CTX, self.n_kv), f32),
-                    np.zeros((CTX, self.n_kv, self.hd), np.int16)) if at else None for at in self.attn]
+        self.kv = [(np.zeros((self.ctx, self.n_kv, self.hd), np.int8), np.zeros((self.ctx, self.n_kv), f32),
+                    np.zeros((self.ctx, self.n_kv, self.hd), np.int16)) if at else None for at in self.attn]
         self.gs = [None if at else (np.zeros((3, self.cd), f32), np.zeros((self.n_v, self.dk, self.dv), f32))
                    for at in self.attn]
 
@@ -62,7 +65,12 @@ class OracleModel:
         K, N = dims
         bits = {v: b for b, v in R.DET.items()}[ty]
         rows = np.frombuffer(data, np.uint8).reshape(N, -1)
-        return oracle.gemm(rows, N, K, bits, xq, sx, mx, y=y, accumulate=acc)
+        if not self.fast:
+            return oracle.gemm(rows, N, K, bits, xq, sx, mx, y=y, accumulate=acc)
+        if name not in self.x86:
+            self.x86[name] = oracle.X86Linear(rows, N, K, bits)
+        v = self.x86[name].gemm(xq, sx, mx)
+        return (y + v).astype(f32) if acc else v
 
     def forward(self, ids):
         t = len(ids)
