@@ -11,8 +11,9 @@ Workload (the prefill config; configs[0] rides along a
 Inputs are resident in HBM before timing.  Each shape rotates over enough weight copies (> 512 MB in total) that
 no launch finds its weights in the 256 MB Infinity Cache.  Kernel time comes from HIP events on the null stream
 (the stream det's kernels run on) around the timed launches.
-The CPU baseline (rank 0, N=1) times the oracle's C GEMM (a port of the reference's scalar path) on a bounded
-sample of the same W6 M=512 workload.
+The CPU baseline (rank 0, N=1) times det's x86 GEMM algorithm restated in C (oracle/x86_gemm.c) on the same
+quantized weights: the W6 M=512 GEMM on all host threads (at most 16) and on one, and the M=1 GEMVs of the W6
+linear and the W8 head, each for a few seconds.
 """
 import argparse
 import ctypes
@@ -68,7 +69,8 @@ def algo_bytes(N, K, M, bits):
 
 
 def make_linear_copies(N, K, bits, seed, min_bytes):
-    """Quantize seeded N(0, 0.02) weights on the device and repack them into enough copies to exceed min_bytes."""
+    """Quantize seeded N(0, 0.02) weights on the device and repack them into enough copies to exceed min_bytes.
+    Returns the linears and the det rows (host copy, for the CPU baseline on the same weights)."""
     w = (np.random.default_rng(seed).standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
     wd = ffi.Buf.upload(w)
     del w
@@ -77,9 +79,9 @@ def make_linear_copies(N, K, bits, seed, min_bytes):
     one = N * row_bytes(bits, K)
     copies = max(1, -(-min_bytes // one))
     lins = [ffi.Linear(None, K, bits, rows_on_device=(rows, N)) for _ in range(copies)]
-    ffi.lib().det_sync()
+    host_rows = rows.download()
     rows.free()
-    return lins
+    return lins, host_rows
 
 
 def make_acts(M, K, seed):
@@ -145,35 +147,68 @@ def cpu_model():
     return 'unknown'
 
 
-def cpu_baseline(target_s=10.0):
-    """det's x86 backend GEMM (crates/det/src/x86/gemm.rs: strips of 8 rows, vpdpbusd on AVX-VNNI, else
-    vpmaddubsw + vpmaddwd; restated in oracle/x86_gemm.c, checked bit for bit against the scalar oracle) on the
-    whole W6 M=512 workload, repeated for about `target_s` seconds on all of the host's threads (at most 16)."""
-    threads = min(os.cpu_count() or 1, 16)
-    threads = int(os.environ.get('OMP_NUM_THREADS', threads))
+def cpu_flags():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('flags'):
+                return set(line.split(':', 1)[1].split())
+    except OSError:
+        pass
+    return set()
+
+
+def cpu_host_acts(M, K, seed):
+    """The bench's activations (N(0,1), every 37th row x1e-3, one zero row) quantized by the oracle."""
     import oracle
-    K, M, N, bits = 2560, 512, 9728, 6
-    rng = np.random.default_rng(11)
-    x = rng.standard_normal((M, K), dtype=np.float32)
+    x = np.random.default_rng(seed).standard_normal((M, K), dtype=np.float32)
     x[::37] *= np.float32(1e-3)
-    x[M // 2] = 0.0
-    xq, sx, mx = oracle.quant(x)
-    rows = oracle.Rng(2560).fake_rows(bits, N, K)
-    X = oracle.X86Linear(rows, N, K, bits)
-    vnni = oracle.has_vnni()
-    X.gemm(xq, sx, mx, vnni=vnni, threads=threads)           # warm-up
+    if M > 1:
+        x[M // 2] = 0.0
+    return oracle.quant(x)
+
+
+def time_cpu(X, xq, sx, mx, threads, vnni, target_s):
+    X.gemm(xq, sx, mx, vnni=vnni, threads=threads)            # warm-up
     reps, t0 = 0, time.perf_counter()
     while True:
         X.gemm(xq, sx, mx, vnni=vnni, threads=threads)
         reps += 1
         dt = time.perf_counter() - t0
         if dt > target_s:
-            break
-    tops = 2.0 * M * N * K * reps / dt / 1e12
+            return dt / reps, reps, dt
+
+
+def cpu_baseline(rows6, rows_head, target_s=5.0):
+    """det's x86 backend GEMM (crates/det/src/x86/gemm.rs: strips of 8 rows, vpdpbusd on AVX-VNNI, else
+    vpmaddubsw + vpmaddwd; restated in oracle/x86_gemm.c, checked bit for bit against the scalar oracle) on the
+    GPU line's own quantized weights: the W6 M=512 GEMM on all of the host's threads (at most 16; `value`) and on
+    one thread, and the M=1 decode GEMVs of the W6 linear and the W8 head in GB/s of algorithmic bytes, each
+    repeated for about `target_s` seconds (det bench --gemm's figures, main.rs:343-423)."""
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    threads = int(os.environ.get('OMP_NUM_THREADS', threads))
+    vnni = oracle.has_vnni()
+    K, M, N, NH = 2560, 512, 9728, 248320
+    X6 = oracle.X86Linear(rows6, N, K, 6)
+    xq, sx, mx = cpu_host_acts(M, K, 2)
+    per, reps, dt = time_cpu(X6, xq, sx, mx, threads, vnni, target_s)
+    tops = 2.0 * M * N * K / per / 1e12
+    per1, reps1, dt1 = time_cpu(X6, xq, sx, mx, 1, vnni, target_s)
+    xq1, sx1, mx1 = cpu_host_acts(1, K, 4)
+    perd, _, _ = time_cpu(X6, xq1, sx1, mx1, threads, vnni, target_s / 2)
+    XH = oracle.X86Linear(rows_head, NH, K, 8)
+    perh, _, _ = time_cpu(XH, xq1, sx1, mx1, threads, vnni, target_s / 2)
+    del XH
+    flags = cpu_flags()
     return {'value': round(tops, 4), 'unit': 'TOPS', 'cores': threads, 'kind': 'port',
-            'sample': f"det's x86 GEMM algorithm (crates/det/src/x86/gemm.rs) restated in C "
-                      f"({'AVX-VNNI vpdpbusd' if vnni else 'AVX2 vpmaddubsw'} path, {cpu_model()}), "
-                      f'the whole W6 K=2560 N=9728 M=512 GEMM {reps} times in {dt:.1f} s'}
+            'cpu': cpu_model(), 'nproc': os.cpu_count(), 'avx_vnni': 'avx_vnni' in flags,
+            'avx512_vnni': 'avx512_vnni' in flags, 'path': 'AVX-VNNI vpdpbusd' if vnni else 'AVX2 vpmaddubsw',
+            'w6_m512_tops_1_thread': round(2.0 * M * N * K / per1 / 1e12, 4),
+            'w6_m1_gbps': round(algo_bytes(N, K, 1, 6) / perd / 1e9, 2),
+            'w8_head_m1_gbps': round(algo_bytes(NH, K, 1, 8) / perh / 1e9, 2),
+            'sample': f"det's x86 GEMM algorithm (crates/det/src/x86/gemm.rs) restated in C on the GPU line's "
+                      f"weights: the whole W6 K=2560 N=9728 M=512 GEMM {reps} times in {dt:.1f} s on {threads} "
+                      f"threads and {reps1} times in {dt1:.1f} s on 1 thread; M=1 GEMVs of it and of the W8 head"}
 
 
 # ---------------------------------------------------------------- end to end (BASELINE.json configs[4])
@@ -322,7 +357,8 @@ def main():
     ev = HipEvents()
     K, N6, NH = 2560, 9728, 248320
 
-    lin6 = make_linear_copies(N6, K, 6, 1, ROTATE_BYTES)
+    lin6, rows6 = make_linear_copies(N6, K, 6, 1, ROTATE_BYTES)
+    rows_head = None
     xq, sx, mx = make_acts(512, K, 2)
     y = ffi.Buf((512, NH), np.float32)
     ms, wall = time_gemm(ev, lin6, xq, sx, mx, 512, y, args.steps, args.warmup)
@@ -337,7 +373,7 @@ def main():
         for l in lin6:
             for b in (l.wq, l.c, l.m):
                 b.free()
-        linh = make_linear_copies(NH, K, 8, 4, ROTATE_BYTES)
+        linh, rows_head = make_linear_copies(NH, K, 8, 4, ROTATE_BYTES)
         for M in (1, 512):
             xq_m, sx_m, mx_m = make_acts(M, K, 5 + M)
             msm, _ = time_gemm(ev, linh, xq_m, sx_m, mx_m, M, y, max(10, args.steps // 10), max(2, args.warmup // 10))
@@ -364,7 +400,9 @@ def main():
     if dec:
         out['decode'] = {s['shape']: {'GBps': s['GBps'], 'frac_of_hbm_peak': s['frac_of_bound'], 'us': s['us']} for s in dec}
     if not args.no_cpu:
-        out['cpu_baseline'] = cpu_baseline()
+        if rows_head is None:
+            rows_head = np.zeros((NH, row_bytes(8, K)), np.uint8)
+        out['cpu_baseline'] = cpu_baseline(rows6, rows_head)
     print(json.dumps(out), flush=True)
 
 

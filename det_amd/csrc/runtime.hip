@@ -1,70 +1,123 @@
-// det HIP runtime: device init, tracked device buffers, synchronization, the primitive test hook.
-// Mirrors the behaviour of the reference runtime (kernels/cuda/runtime.cu:83-127): det_malloc zero-fills and
-// returns NULL on failure, det_free waits for pending work and aborts on a foreign pointer, det_sync aborts on a
-// kernel error.  One in-order stream: the null stream.
+// Runtime half of det's C ABI on HIP: the device, the buffers det_malloc hands out, synchronisation, copies and the
+// elementwise primitive test hook.  The behaviour the ABI fixes (reference det_cuda.h:15-24, runtime.cu:83-128):
+//   * det_malloc returns a zero-filled device buffer, or NULL (with a message) when the device cannot provide it;
+//   * det_free accepts NULL (and anything before the first det_malloc or det_init), refuses (message, abort) a
+//     pointer det_malloc did not return, and waits for the device before releasing, since launches still in flight
+//     may read the buffer;
+//   * det_sync waits for the device and aborts when a kernel failed;
+//   * every operation runs on the null stream, det's one in-order stream.
+#include <algorithm>
+#include <map>
 #include <mutex>
+#include <string>
 #include <string.h>
-#include <unordered_map>
 #include "common.h"
 #include "../../include/det_hip.h"
 using namespace det;
 
 namespace {
 
-struct Ctx {
-    int dev = 0;
-    char name[256] = {0};
-    std::mutex mu;
-    std::unordered_map<void*, size_t> allocs;
-    size_t allocated = 0;
-};
-Ctx* g = nullptr;
-std::once_flag g_once;
-
-void init_once() {
-    g = new Ctx();
-    DET_CHECK(hipGetDevice(&g->dev));
-    hipDeviceProp_t p;
-    DET_CHECK(hipGetDeviceProperties(&p, g->dev));
-    snprintf(g->name, sizeof g->name, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
-}
-inline void ensure_init() { std::call_once(g_once, init_once); }
-
-// ---- test hook kernels: op numbers as documented in det_hip.h
-__global__ void k_prim(int op, const float* __restrict__ x, int n, float* __restrict__ out) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float v = x[i];
-    const float w = x[n - 1 - i];
-    float r = 0.0f;
-    switch (op) {
-        case 0: r = exp_f(v); break;
-        case 1: r = log_f(v); break;
-        case 2: r = softplus_f(v); break;
-        case 3: r = sigmoid_f(v); break;
-        case 4: r = silu_f(v); break;
-        case 5: case 12: {
-            if (i & 1) return;
-            const unsigned long long lo = __float_as_uint(v), hi = __float_as_uint(x[i + 1]);
-            const long long q = (long long)((hi << 32) | lo);
-            r = op == 5 ? i64_to_f(q) : (float)q;
-            break;
-        }
-        case 6: r = rint_(v); break;
-        case 7: r = 1.0f / v; break;
-        case 8: r = __builtin_sqrtf(v); break;
-        case 9: r = v * w; break;
-        case 10: r = v + w; break;
-        case 13: r = (float)f2i_sat(rint_(v)); break;
-        case 14: r = v / w; break;
-        case 15: r = v - w; break;
-        case 16: r = fmax_spec(v, w); break;
-        default: r = v;
+// The process's view of the device: which one, what it is called, and every live det_malloc block (start address ->
+// size), so that det_free can tell its own pointers from foreign ones and det_allocated_bytes can report the total.
+class DeviceState {
+public:
+    static DeviceState& instance() {
+        static DeviceState s;           // constructed on first use, once, even with concurrent first callers
+        return s;
     }
-    out[i] = r;
+    const char* label() const { return label_.c_str(); }
+
+    void* allocate(size_t bytes) {
+        const size_t want = bytes ? bytes : 1;            // a zero-byte request still gets a distinct block
+        void* p = nullptr;
+        const hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();                      // the failure is reported here, not by the next call
+            fprintf(stderr, "det_malloc: %zu bytes not available on the device (%s)\n", bytes, hipGetErrorString(e));
+            return nullptr;
+        }
+        DET_CHECK(hipMemsetAsync(p, 0, want, nullptr));
+        std::lock_guard<std::mutex> hold(mu_);
+        blocks_.emplace(reinterpret_cast<uintptr_t>(p), want);
+        live_ += want;
+        return p;
+    }
+
+    // false: p is not the start of a live block
+    bool forget(void* p) {
+        std::lock_guard<std::mutex> hold(mu_);
+        const auto it = blocks_.find(reinterpret_cast<uintptr_t>(p));
+        if (it == blocks_.end()) return false;
+        live_ -= it->second;
+        blocks_.erase(it);
+        return true;
+    }
+
+    size_t live() {
+        std::lock_guard<std::mutex> hold(mu_);
+        return live_;
+    }
+
+private:
+    DeviceState() {
+        int dev = 0;
+        DET_CHECK(hipGetDevice(&dev));
+        hipDeviceProp_t prop;
+        DET_CHECK(hipGetDeviceProperties(&prop, dev));
+        label_ = std::string(prop.name) + " (" + prop.gcnArchName + ", " + std::to_string(prop.multiProcessorCount) +
+                 " CUs)";
+    }
+    std::string label_;
+    std::mutex mu_;
+    std::map<uintptr_t, size_t> blocks_;
+    size_t live_ = 0;
+};
+
+bool g_touched = false;     // set once the device state exists: det_free and det_allocated_bytes never create it
+
+DeviceState& device() {
+    DeviceState& d = DeviceState::instance();
+    g_touched = true;
+    return d;
 }
 
-// spec treesum (spec/prim.rs:154-170) of each row of n <= 8192, padded with +0 to p = next power of two:
+// ---- det_test_prim: ops as numbered in det_hip.h.  Binary ops pair element i with element n - 1 - i.
+__device__ float prim_one(int op, float a, float b) {
+    switch (op) {
+        case 0: return exp_f(a);
+        case 1: return log_f(a);
+        case 2: return softplus_f(a);
+        case 3: return sigmoid_f(a);
+        case 4: return silu_f(a);
+        case 6: return rint_(a);
+        case 7: return 1.0f / a;
+        case 8: return __builtin_sqrtf(a);
+        case 9: return a * b;
+        case 10: return a + b;
+        case 13: return (float)f2i_sat(rint_(a));
+        case 14: return a / b;
+        case 15: return a - b;
+        case 16: return fmax_spec(a, b);
+        default: return a;
+    }
+}
+
+__global__ void k_prim_elementwise(int op, const float* __restrict__ x, int n, float* __restrict__ out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = prim_one(op, x[i], x[n - 1 - i]);
+}
+
+// ops 5 and 12: the int64 whose low / high 32 bits are the fp32 bit patterns x[2j] / x[2j + 1], converted to fp32
+// into out[2j] (5: the library's RNE routine i64_to_f, 12: the compiler's conversion); odd entries are left as they are
+__global__ void k_prim_int64(int op, const float* __restrict__ x, int pairs, float* __restrict__ out) {
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < pairs; j += gridDim.x * blockDim.x) {
+        const unsigned long long bits = (unsigned long long)__float_as_uint(x[2 * j + 1]) << 32 | __float_as_uint(x[2 * j]);
+        const long long v = (long long)bits;
+        out[2 * j] = op == 5 ? i64_to_f(v) : (float)v;
+    }
+}
+
+// op 11: the spec treesum (spec/prim.rs:154-170) of each row of n <= 8192, padded with +0 to p = next power of two:
 // each thread reduces 8 contiguous values as a local tree, then the p/8 partials are combined pairwise by
 // ascending distance through LDS -- the same balanced tree.  Rows of p <= 8 run the tree in one thread.
 __global__ void __launch_bounds__(1024) k_prim_treesum(const float* __restrict__ x, int n, float* __restrict__ out) {
@@ -101,63 +154,56 @@ __global__ void __launch_bounds__(1024) k_prim_treesum(const float* __restrict__
     if (t == 0) out[blockIdx.x] = s[0];
 }
 
+unsigned grid_for(size_t items) { return (unsigned)std::min<size_t>((items + 255) / 256, 65535); }
+
 } // namespace
 
 extern "C" {
 
-int det_init(void) { ensure_init(); return g ? 0 : 1; }
-const char* det_device_name(void) { ensure_init(); return g->name; }
-void* det_hip_stream(void) { ensure_init(); return (void*)(hipStream_t)0; }
+int det_init(void) { device(); return 0; }
+const char* det_device_name(void) { return device().label(); }
+void* det_hip_stream(void) { device(); return nullptr; }          // the null stream
 
-void* det_malloc(size_t bytes) {
-    ensure_init();
-    if (bytes == 0) bytes = 16;
-    void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) {
-        (void)hipGetLastError();
-        fprintf(stderr, "det_malloc(%zu) failed\n", bytes);
-        return NULL;
-    }
-    DET_CHECK(hipMemsetAsync(p, 0, bytes, 0));
-    std::lock_guard<std::mutex> lock(g->mu);
-    g->allocs[p] = bytes;
-    g->allocated += bytes;
-    return p;
-}
+void* det_malloc(size_t bytes) { return device().allocate(bytes); }
 
 void det_free(void* p) {
-    if (!p || !g) return;
-    {
-        std::lock_guard<std::mutex> lock(g->mu);
-        auto it = g->allocs.find(p);
-        if (it == g->allocs.end()) { fprintf(stderr, "det_free: %p is not a det_malloc pointer\n", p); abort(); }
-        g->allocated -= it->second;
-        g->allocs.erase(it);
+    if (!p || !g_touched) return;            // nothing was ever allocated: nothing to release
+    if (!device().forget(p)) {
+        fprintf(stderr, "det_free: %p was not returned by det_malloc (or was freed already)\n", p);
+        abort();
     }
-    DET_CHECK(hipDeviceSynchronize());   // pending work may still read the buffer
+    DET_CHECK(hipDeviceSynchronize());        // launches still in flight may read the block
     DET_CHECK(hipFree(p));
 }
 
-size_t det_allocated_bytes(void) { return g ? g->allocated : 0; }
+size_t det_allocated_bytes(void) { return g_touched ? device().live() : 0; }
 
 void det_sync(void) {
-    ensure_init();
+    device();
     const hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) { fprintf(stderr, "det (hip) fatal: %s\n", hipGetErrorString(e)); abort(); }
+    if (e != hipSuccess) {
+        fprintf(stderr, "det_sync: the device reported an error: %s\n", hipGetErrorString(e));
+        abort();
+    }
 }
-void det_flush(void) {}
+
+void det_flush(void) {}       // launches are submitted as they are made
 
 void det_memset(void* p, int value, size_t bytes, hipStream_t st) { DET_CHECK(hipMemsetAsync(p, value, bytes, st)); }
+
 void det_memcpy(void* dst, const void* src, size_t bytes, hipStream_t st) {
     DET_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, st));
 }
 
 void det_test_prim(int op, const float* x, int M, int n, float* out, hipStream_t st) {
+    const size_t total = (size_t)M * n;
     if (op == 11) {
         if (n > 8192) { fprintf(stderr, "det_test_prim: treesum rows are limited to 8192 (n=%d)\n", n); abort(); }
         k_prim_treesum<<<M, 1024, 0, st>>>(x, n, out);
+    } else if (op == 5 || op == 12) {
+        k_prim_int64<<<grid_for(total / 2), 256, 0, st>>>(op, x, (int)(total / 2), out);
     } else {
-        k_prim<<<(unsigned)(((size_t)M * n + 255) / 256), 256, 0, st>>>(op, x, (int)((size_t)M * n), out);
+        k_prim_elementwise<<<grid_for(total), 256, 0, st>>>(op, x, (int)total, out);
     }
     DET_CHECK(hipGetLastError());
 }

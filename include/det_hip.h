@@ -1,12 +1,13 @@
 // det_hip.h -- C API of det's quantized-linear path on AMD Instinct MI355X (gfx950, HIP).
 //
-// Drop-in for the GEMM / activation-quantization / runtime part of det's CUDA C API
-// (reference kernels/cuda/det_cuda.h).  Names, argument meaning and error behaviour are the same; the
-// only type change is hipStream_t for cudaStream_t, and det_hip_stream for det_cuda_stream.
-//   * every pointer is a DEVICE pointer (det_malloc); the host moves data with det_memcpy;
-//   * hipStream_t 0 (the null stream) is the one in-order stream; det_sync waits for the whole device;
-//   * compute calls return nothing: an invalid shape prints a message and aborts, as in the reference.
-// Row-major layouts, fp32 unless noted.
+// A drop-in for the GEMM, activation-quantization and runtime entry points of det's CUDA C API (reference
+// kernels/cuda/det_cuda.h): the same names, argument meanings and error behaviour, with hipStream_t in place of
+// cudaStream_t and det_hip_stream in place of det_cuda_stream.  Conventions of this header:
+//   * pointers to tensors live in device memory obtained from det_malloc; det_memcpy moves data to and from the host;
+//   * det runs everything on the null stream, in order; det_sync waits for the whole device;
+//   * compute entry points return nothing: arguments outside what they accept are reported on stderr and the
+//     process aborts, as the reference does.
+// Tensors are row-major; element types are fp32 unless a declaration says otherwise.
 #pragma once
 #include <stdint.h>
 #include <stddef.h>
@@ -33,7 +34,9 @@ void*       det_hip_stream(void);           // the stream det's work runs on (de
 //   wq: packed codes in 64-row tiles, [T][K/128][GB/16][64 rows][16 bytes] with T = 2*ceil(N/128) (whole pairs of
 //       tiles), where GB = 128, 96, 64 bytes is one row's packed 128-group (4 * bytes_per_32) for W8, W6, W4; the
 //       16-byte chunk c of a tile row is bytes [16c, 16c+16) of that row's packed group, exactly as in the det row;
-//       rows past N are zero;
+//       rows past N are zero.  The same number of bytes follows: the prefill planes, per 32-row block and 128-group
+//       one 16-byte word per lane and plane (4, 3, 2 planes for W8, W6, W4), holding the codes of one row and
+//       k-half in the order and scaled packing the M > 64 kernel feeds to the matrix core;
 //   c:  [T*64] fp32 (zero past N);
 //   m:  [T][K/128][64] uint16 (zero past N).
 typedef struct {
@@ -118,8 +121,8 @@ size_t det_gdn_scratch_bytes(int M, int n_k, int n_v, int dk, int dv);
 // the largest of logits[m][0 .. V)
 void det_argmax(const float* logits, int M, int V, int* out, hipStream_t st);
 
-// ---- test hooks (replaces det_test_prim of runtime.cu; det_cuda.h:114-118): elementwise fp32 primitives on arrays,
-// for bit-exactness tests vs the spec.
+// ---- test hooks (det_test_prim of runtime.cu; det_cuda.h:114-118): the spec's fp32 primitives applied to an array,
+// so that tests can compare them bit for bit with the spec.
 // op: 0 exp_f, 1 log_f, 2 softplus_f, 3 sigmoid_f, 4 silu_f, 5 i64->f32 of (long long) bits of x pairs (x[2i],x[2i+1]),
 //     6 rint, 7 1/x, 8 sqrt, 9 x*y (y = x reversed), 10 x+y, 11 treesum of each row of n (out[M]), 12 native i64->f32,
 //     13 rint as int, 14 x/y, 15 x-y, 16 max(x,y)
