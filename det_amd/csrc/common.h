@@ -22,6 +22,13 @@ __host__ __device__ constexpr int group_bytes(int bits) { return 4 * bpl(bits); 
 // tile geometry of the repacked layout: 64 rows per tile, 16-byte chunks
 constexpr int TILE_N = 64;
 
+// Hand-over between the workgroups of one launch (K-slices, split tiles, last-arriver epilogues): the producer writes
+// its results with agent-scope atomic operations, which are performed at the device-coherent level instead of
+// staying dirty in one XCD's L2; this wait blocks until every memory operation of the wave has been performed, and
+// the memory clobber keeps the compiler from moving loads or stores across it.  Only then is the arrival counter
+// bumped, and the consumer that sees the final count reads with agent-scope atomic loads.
+__device__ __forceinline__ void wait_performed() { asm volatile("s_waitcnt 0" ::: "memory"); }
+
 __device__ __forceinline__ float fmax_spec(float a, float b) {   // spec/prim.rs:58-70 (-0 below +0, NaN wins)
     if (__builtin_isnan(a) || __builtin_isnan(b)) return __builtin_isnan(a) ? a : b;
     if (a > b || (a == b && __builtin_signbit(b))) return a;

@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(64 * dec_maxw<MP>()) k_decode(const uint8_t* _
         if (KS > 1 && t < M) __hip_atomic_fetch_add(part + (size_t)t * npad + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (KS > 1) {
-        __builtin_amdgcn_s_waitcnt(0);             // this wave's adds have been performed
+        wait_performed();             // this wave's adds have been performed
         __syncthreads();
         if (threadIdx.x == 0)
             last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);
@@ -456,7 +456,7 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
             const int t = wv + W * i;
             if (t < mt) __hip_atomic_store(mine + (size_t)t * npad + n, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        __builtin_amdgcn_s_waitcnt(0);             // this wave's stores have been performed
+        wait_performed();             // this wave's stores have been performed
         __syncthreads();
         if (threadIdx.x == 0)
             last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);

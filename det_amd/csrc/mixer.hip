@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(RT) k_attn_acc(const int8_t* __restrict__ kq, 
     }
     if (!FIN) return;
     // the row's last chunk to arrive writes the output (its sums are complete once every chunk's adds are performed)
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_performed();
     __syncthreads();
     if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(S.cnt + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)((nkeys + CK - 1) / CK - 1);
@@ -857,7 +857,7 @@ __global__ void __launch_bounds__(GT) k_gdn_rec(float* __restrict__ S, const flo
     if (!cnt) return;
     // one token (cnt != NULL): the head's last column block to count itself runs the gated norm (k_gdn_out) on the
     // head's output, which every block stored with agent-scope stores that have been performed
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_performed();
     __syncthreads();
     if (tid == 0) last = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
     __syncthreads();

@@ -410,7 +410,7 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                 for (int r = 0; r < 16; r++)
                     __hip_atomic_store(mine + ((wv * 4 + j) * 16 + r) * 64 + lane, (long long)U[j][r], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // this wave's stores have been performed
+            wait_performed();                      // this wave's stores have been performed
             __syncthreads();
             if (tid == 0)
                 last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(wl - wf);
@@ -732,7 +732,7 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
 #pragma unroll
             for (int r = 0; r < 16; r++)
                 __hip_atomic_store(at(ks, j, r), (long long)U[j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);             // this wave's stores have been performed
+        wait_performed();             // this wave's stores have been performed
         __syncthreads();
         if (tid == 0)
             last_s = __hip_atomic_fetch_add(cnt + tcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(KS - 1);
