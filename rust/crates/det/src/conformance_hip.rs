@@ -4,7 +4,8 @@
 // Every width through every batch-size path on activation rows that are all zero, made of denormals, scaled by
 // 1e-3 or ordinary; quantized by the CPU backend (quant_act_i8g) and multiplied on both backends, bit for bit.  Then
 // int64 -> fp32 rounding ties in the epilogue: one nonzero code and one nonzero activation per row, with the
-// multipliers chosen so that acc = m * mx lands on 2^24 + 1 and 2^24 + 3 (round to even, down and up), of both signs.
+// multipliers chosen so that acc = m * mx lands on 2^24 + 1 and 2^24 + 3 (round to even, down and up), of both signs
+// (the second group's activations are zero, so only group 0 contributes).
 // UNVERIFIED: no Rust toolchain was available where this was written; the same cases run through the C ABI in the
 // repository's tests (tests/test_gemm_parity.py: test_edge_rows, test_int64_to_fp32_ties).
 
@@ -41,18 +42,20 @@ pub fn gemm_edges<B: Backend>(gpu: &B, r: &mut Report) {
             }
         }
     }
-    // ties: W8 rows whose only nonzero code is +-1 at k = 0, c = 1, m = 24929; activation rows whose only nonzero
-    // code is 1 at k = 0, sx = 1, mx = 673 or 2019, so acc = +-16777217 or +-50331651 (2^24 + 1, 3 * 2^24 + 3)
+    // ties: W8 rows whose only nonzero code is +-1 at k = 0, c = 1, m = 24929 (even rows) or 10831 (odd rows);
+    // activation rows whose only nonzero code is 1 at k = 0, sx = 1, mx = 673 (even tokens) or 1549 (odd tokens):
+    // acc = 24929 * 673 = 2^24 + 1 (ties to 2^24) and 10831 * 1549 = 2^24 + 3 (ties to 2^24 + 4), of both signs
     let k = 256;
     let rb = GgmlType::Det8.row_bytes(k);
     let n = 64;
     let mut data = vec![0u8; n * rb];
     for row in 0..n {
         let d = &mut data[row * rb..(row + 1) * rb];
-        d[0] = if row % 2 == 0 { 1 } else { (-1i8) as u8 };
+        d[0] = if row % 4 < 2 { 1 } else { (-1i8) as u8 };
         d[k..k + 4].copy_from_slice(&1.0f32.to_le_bytes());
         for gi in 0..k / 128 {
-            d[k + 4 + 2 * gi..k + 6 + 2 * gi].copy_from_slice(&24929u16.to_le_bytes());
+            let m: u16 = if row % 2 == 0 { 24929 } else { 10831 };
+            d[k + 4 + 2 * gi..k + 6 + 2 * gi].copy_from_slice(&m.to_le_bytes());
         }
     }
     let g = tie_gguf(&data, n, k);
@@ -63,10 +66,10 @@ pub fn gemm_edges<B: Backend>(gpu: &B, r: &mut Report) {
         let sx: Buf<f32> = cpu.alloc(m);
         let mx: Buf<u16> = cpu.alloc(m * k / 128);
         for t in 0..m {
-            xq.host_mut()[t * k] = 1;
+            xq.host_mut()[t * k] = 1;              // group 1 stays zero
             sx.host_mut()[t] = 1.0;
             for gi in 0..k / 128 {
-                mx.host_mut()[t * (k / 128) + gi] = if t % 2 == 0 { 673 } else { 2019 };
+                mx.host_mut()[t * (k / 128) + gi] = if t % 2 == 0 { 673 } else { 1549 };
             }
         }
         let yc: Buf<f32> = cpu.alloc(m * n);
