@@ -346,3 +346,16 @@ bool mul_quant(const float* a, const float* b, int M, int n, int8_t* xq, float* 
 }
 
 } // namespace det
+
+extern "C" {
+
+void det_test_gemv_silu0(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int nparts,
+                         const int* offs, float* const* dsts, hipStream_t st) {
+    det::gemm_parts_silu0(L, xq, sx, mx, nparts, offs, dsts, st);
+}
+
+void det_test_mul_quant(const float* a, const float* b, int M, int n, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st) {
+    if (!det::mul_quant(a, b, M, n, xq, sx, mx, st)) DET_FAIL("det_test_mul_quant: unsupported row of n=%d", n);
+}
+
+} // extern "C"

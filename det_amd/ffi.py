@@ -76,6 +76,8 @@ def lib():
         'det_gemm_ex': (None, [ctypes.POINTER(QLinear), P, P, P, i, P, i, i, P, P, P]),
         'det_gemm_scratch_bytes': (sz, [i, i]), 'det_gemm_set_scratch': (None, [P, sz]),
         'det_test_prim': (None, [i, P, i, i, P, P]),
+        'det_test_gemv_silu0': (None, [ctypes.POINTER(QLinear), P, P, P, i, P, P, P]),
+        'det_test_mul_quant': (None, [P, P, i, i, P, P, P, P]),
         'det_attention': (None, [ctypes.POINTER(AttnLayer), ctypes.POINTER(KvCache), P, P, P, P, P, i, f, i, i, i, i,
                                  i, P, P, P]),
         'det_attn_scratch_bytes': (sz, [i, i, i]),

@@ -127,6 +127,14 @@ void det_argmax(const float* logits, int M, int V, int* out, hipStream_t st);
 //     6 rint, 7 1/x, 8 sqrt, 9 x*y (y = x reversed), 10 x+y, 11 treesum of each row of n (out[M]), 12 native i64->f32,
 //     13 rint as int, 14 x/y, 15 x-y, 16 max(x,y)
 void det_test_prim(int op, const float* x, int M, int n, float* out, hipStream_t st);
+// Test hooks of the model runner's one-token FFN path (no det_cuda.h counterpart; for tests of this library):
+//   det_test_gemv_silu0: det_gemm_ex with M = 1 and Parts output (2 to 4 parts from column 0), storing silu_f(v)
+//     instead of v for the columns of part 0 (the gate half of a fused gate|up linear);
+//   det_test_mul_quant: h = a * b per element, quantized in group mode (n % 128 == 0, n <= 32768): with a = silu_f(g)
+//     the same codes and scales as det_silu_mul_quant(g, b).  Other shapes abort.
+void det_test_gemv_silu0(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int nparts,
+                         const int* offs, float* const* dsts, hipStream_t st);
+void det_test_mul_quant(const float* a, const float* b, int M, int n, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st);
 
 #ifdef __cplusplus
 }

@@ -170,12 +170,11 @@ def prefill_accesses(N, K, M, bits, cus=256):
                     assert len(lo) == int(((t0 + sidx) < M).sum())
 
 
-SHAPES = [(640, 2560), (9728, 2560), (2560, 9728), (200, 384), (48, 128), (17408, 5120), (5120, 17408), (64, 2560),
-          (10240, 2560)]
+SHAPES = [(640, 2560), (9728, 2560), (2560, 9728), (200, 384), (48, 128), (5120, 17408), (64, 2560)]
 
 
 @pytest.mark.parametrize('bits', [4, 6, 8])
 @pytest.mark.parametrize('N,K', SHAPES)
 def test_prefill_accesses_in_bounds(N, K, bits):
-    for M in (65, 100, 128, 300, 512):
+    for M in (65, 300, 512):
         prefill_accesses(N, K, M, bits)
