@@ -111,6 +111,33 @@ def time_gemm(ev, lins, xq, sx, mx, M, y, steps, warmup):
     return ms / steps, wall
 
 
+def read_floor(ev, nbytes, steps=200, grids=(512, 1024, 2048, 4096)):
+    """The fastest plain streaming read (det_test_read) of `nbytes`, rotating over copies that exceed the Infinity
+    Cache, over a few grid sizes: the floor a single-pass read of a GEMV's weight bytes can reach at that size.
+    Returns (us, GB/s, grid)."""
+    nb = (nbytes + 15) // 16 * 16
+    copies = max(1, -(-ROTATE_BYTES // nb))
+    bufs = [ffi.Buf(nb, np.uint8) for _ in range(copies)]
+    sink = ffi.Buf(max(grids), np.uint32)
+    L = ffi.lib()
+    best = None
+    for grid in grids:
+        for i in range(10):
+            L.det_test_read(bufs[i % copies].ptr, nb, grid, sink.ptr, None)
+        a, b = ev.event(), ev.event()
+        ev.record(a)
+        for i in range(steps):
+            L.det_test_read(bufs[i % copies].ptr, nb, grid, sink.ptr, None)
+        ev.record(b)
+        us = ev.elapsed_ms(a, b) * 1e3 / steps
+        if best is None or us < best[0]:
+            best = (us, nbytes / us / 1e3, grid)
+    for b_ in bufs:
+        b_.free()
+    sink.free()
+    return best
+
+
 def shape_line(name, N, K, M, bits, ms):
     ops = 2.0 * M * N * K
     byt = algo_bytes(N, K, M, bits)
@@ -398,7 +425,14 @@ def main():
     }
     dec = [s for s in shapes if s['M'] == 1]
     if dec:
-        out['decode'] = {s['shape']: {'GBps': s['GBps'], 'frac_of_hbm_peak': s['frac_of_bound'], 'us': s['us']} for s in dec}
+        out['decode'] = {}
+        for s_ in dec:
+            wbytes = s_['N'] * row_bytes(s_['bits'], s_['K'])
+            fus, fgbs, fgrid = read_floor(ev, wbytes)
+            out['decode'][s_['shape']] = {
+                'GBps': s_['GBps'], 'frac_of_hbm_peak': s_['frac_of_bound'], 'us': s_['us'],
+                'read_floor_us': round(fus, 3), 'read_floor_GBps': round(fgbs, 1), 'read_floor_grid': fgrid,
+                'frac_of_read_floor': round(fus / s_['us'], 4)}
     if not args.no_cpu:
         if rows_head is None:
             rows_head = np.zeros((NH, row_bytes(8, K)), np.uint8)

@@ -154,6 +154,36 @@ __global__ void __launch_bounds__(1024) k_prim_treesum(const float* __restrict__
     if (t == 0) out[blockIdx.x] = s[0];
 }
 
+// det_test_read: a plain streaming read, the measuring stick for the HBM-bound GEMV.  Workgroup b reads its
+// contiguous share of the buffer with 16-byte nontemporal loads, four in flight per thread, and stores the xor of
+// everything it read into sink[b] (so that no load can be dropped).
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(256) k_read(const v4u* __restrict__ p, size_t n16, unsigned* __restrict__ sink) {
+    __shared__ unsigned red[256];
+    const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const size_t lo = (size_t)blockIdx.x * per, hi = lo + per < n16 ? lo + per : n16;
+    unsigned acc = 0;
+    size_t i = lo + threadIdx.x;
+    for (; i + 3 * 256 < hi; i += 4 * 256) {
+        v4u v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = __builtin_nontemporal_load(p + i + u * 256);
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < hi; i += 256) {
+        const v4u v = __builtin_nontemporal_load(p + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned r = 0;
+        for (int t = 0; t < 256; t++) r ^= red[t];
+        sink[blockIdx.x] = r;
+    }
+}
+
 unsigned grid_for(size_t items) { return (unsigned)std::min<size_t>((items + 255) / 256, 65535); }
 
 } // namespace
@@ -193,6 +223,12 @@ void det_memset(void* p, int value, size_t bytes, hipStream_t st) { DET_CHECK(hi
 
 void det_memcpy(void* dst, const void* src, size_t bytes, hipStream_t st) {
     DET_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, st));
+}
+
+void det_test_read(const void* p, size_t bytes, int blocks, unsigned* sink, hipStream_t st) {
+    if (bytes % 16 || blocks < 1) DET_FAIL("det_test_read: bytes must be a multiple of 16 and blocks positive");
+    k_read<<<blocks, 256, 0, st>>>(static_cast<const v4u*>(p), bytes / 16, sink);
+    DET_CHECK(hipGetLastError());
 }
 
 void det_test_prim(int op, const float* x, int M, int n, float* out, hipStream_t st) {

@@ -78,6 +78,7 @@ def lib():
         'det_test_prim': (None, [i, P, i, i, P, P]),
         'det_test_gemv_silu0': (None, [ctypes.POINTER(QLinear), P, P, P, i, P, P, P]),
         'det_test_mul_quant': (None, [P, P, i, i, P, P, P, P]),
+        'det_test_read': (None, [P, sz, i, P, P]),
         'det_attention': (None, [ctypes.POINTER(AttnLayer), ctypes.POINTER(KvCache), P, P, P, P, P, i, f, i, i, i, i,
                                  i, P, P, P]),
         'det_attn_scratch_bytes': (sz, [i, i, i]),

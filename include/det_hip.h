@@ -135,6 +135,10 @@ void det_test_prim(int op, const float* x, int M, int n, float* out, hipStream_t
 void det_test_gemv_silu0(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int nparts,
                          const int* offs, float* const* dsts, hipStream_t st);
 void det_test_mul_quant(const float* a, const float* b, int M, int n, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st);
+// Test hook for measurement (no det_cuda.h counterpart): a plain streaming read of `bytes` (a multiple of 16) of
+// device memory by `blocks` workgroups, each storing the xor of its contiguous share into sink[block]; bench.py
+// times it as the floor a single-pass read of a GEMV's weight bytes can reach.
+void det_test_read(const void* p, size_t bytes, int blocks, unsigned* sink, hipStream_t st);
 
 #ifdef __cplusplus
 }
