@@ -27,9 +27,9 @@ def test_gemv_silu0(bits, widths, K):
     outs = [ffi.Buf((1, w), np.float32) for w in widths]
     offs = (ctypes.c_int * len(widths))(*np.cumsum([0] + list(widths[:-1])).tolist())
     dsts = (ctypes.c_void_p * len(widths))(*[o.ptr for o in outs])
-    ffi.lib().det_test_gemv_silu0(ctypes.byref(lin.q), ffi.Buf.upload(xq).ptr, ffi.Buf.upload(sx).ptr,
-                                  ffi.Buf.upload(mx).ptr, len(widths), ctypes.cast(offs, ctypes.c_void_p),
-                                  ctypes.cast(dsts, ctypes.c_void_p), None)
+    xb, sb, mb = ffi.Buf.upload(xq), ffi.Buf.upload(sx), ffi.Buf.upload(mx)     # held until the call returns
+    ffi.lib().det_test_gemv_silu0(ctypes.byref(lin.q), xb.ptr, sb.ptr, mb.ptr, len(widths),
+                                  ctypes.cast(offs, ctypes.c_void_p), ctypes.cast(dsts, ctypes.c_void_p), None)
     want = oracle.gemm(rows, N, K, bits, xq, sx, mx, widths=list(widths))
     silu = oracle.lib().ora_silu_f
     want[0] = np.array([[silu(float(v)) for v in want[0][0]]], np.float32)
