@@ -38,7 +38,7 @@ def test_gemv_silu0(bits, widths, K):
         assert d is None, f'part {p}: {d}'
 
 
-@pytest.mark.parametrize('n', [128, 2560, 9728, 17408])
+@pytest.mark.parametrize('n', [2560, 9728, 17408])
 def test_mul_quant_equals_silu_mul_quant(n):
     print(f'mul_quant n={n}', flush=True)
     rng = np.random.default_rng(n)
