@@ -243,7 +243,7 @@ QWEN35_4B = dict(hidden=2560, layers=32, interval=4, ff=9728, heads=16, kv=4, hd
                  dv=128, vocab=248320, ctx=640)
 
 
-def write_qwen35_bf16(path, cfg, seed):
+def write_qwen35_bf16(path, cfg, seed, progress=None):
     """A random-init qwen35 float GGUF of the given architecture (weights seeded N(0, 0.02), norms 1 + N(0, 0.02),
     ssm_a negative), BF16 matrices and F32 vectors, streamed to disk tensor by tensor."""
     import struct
@@ -300,7 +300,11 @@ def write_qwen35_bf16(path, cfg, seed):
             data = (a.view(np.uint32) >> 16).astype(np.uint16).tobytes() if kind == 'w' else a.tobytes()
             f.write(data + bytes(-len(data) % 32))
             if idx % 40 == 0:
-                print(f'e2e: writing tensor {idx} of {len(ts)}', file=sys.stderr, flush=True)
+                msg = f'e2e: writing tensor {idx} of {len(ts)}'
+                if progress:
+                    progress(msg)
+                else:
+                    print(msg, file=sys.stderr, flush=True)
 
 
 def e2e(args):

@@ -33,10 +33,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def log(msg, t0=[time.time()]):
     line = f'[{time.time() - t0[0]:7.1f}s] {msg}'
     print(line, flush=True)
-    d = os.path.join(ROOT, 'gpurun_out')
-    if os.path.isdir(d):
-        with open(os.path.join(d, 'test_model_4b.log'), 'a') as f:
-            f.write(line + '\n')
+    d = os.path.join(ROOT, 'gpurun_out')          # a file that keeps growing shows a long run is alive
+    os.makedirs(d, exist_ok=True)
+    with open(os.path.join(d, 'test_model_4b.log'), 'a') as f:
+        f.write(line + '\n')
 
 
 @pytest.mark.timeout(1500)
@@ -44,7 +44,7 @@ def test_qwen35_4b_prefill_512_and_greedy_decode(tmp_path):
     cfg = dict(bench.QWEN35_4B)
     src, dst = tmp_path / 'q35-4b-BF16.gguf', tmp_path / 'q35-4b-det.gguf'
     log('writing the bf16 source')
-    bench.write_qwen35_bf16(str(src), cfg, seed=5)
+    bench.write_qwen35_bf16(str(src), cfg, seed=5, progress=log)
     log(f'converting ({os.path.getsize(src) / 1e9:.2f} GB)')
     gguf.convert(str(src), str(dst), None, cfg['ctx'])
     data = dst.read_bytes()
