@@ -30,6 +30,12 @@ sys.path.insert(0, ROOT)
 from det_amd import ffi  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# the kernel det_gemm_ex runs for the bench's M = 512 line (DET_PREFILL=streamk selects the stream-K kernel) and its
+# grid (total threads, as rocprofv3 reports it) for the committed traffic summary
+if os.environ.get('DET_PREFILL') == 'streamk':
+    PREFILL_KERNEL, PREFILL_GRID = 'k_prefill<6>', 512 * 256
+else:
+    PREFILL_KERNEL, PREFILL_GRID = 'k_prefill2<6>', ((9728 + 63) // 64) * 4 * 256
 INT8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 600 << 20
 
@@ -420,10 +426,10 @@ def main():
                    'M': 512, 'N': N6, 'K': K, 'bits': 6, 'device': device},
         'roofline': {'bound': 'mfma', 'achieved': tops, 'peak': INT8_PEAK_TOPS, 'unit': 'TFLOP/s',
                      'frac': round(tops / INT8_PEAK_TOPS, 4),
-                     'traffic': committed_traffic('k_prefill2<6>', ((N6 + 63) // 64) * 4 * 256),
+                     'traffic': committed_traffic(PREFILL_KERNEL, PREFILL_GRID),
                      'traffic_source': 'profiles/gemm_hbm_traffic.md (FETCH_SIZE x2 + WRITE_SIZE x1 per launch)',
                      'algorithmic_bytes_per_launch': algo_bytes(N6, K, 512, 6),
-                     'kernel': 'k_prefill2<6>', 'algorithmic_ops_per_launch': 2 * 512 * N6 * K},
+                     'kernel': PREFILL_KERNEL, 'algorithmic_ops_per_launch': 2 * 512 * N6 * K},
         'shapes': shapes,
         'timed_wall_s': round(wall, 4),
     }
