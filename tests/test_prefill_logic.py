@@ -178,3 +178,63 @@ SHAPES = [(640, 2560), (9728, 2560), (2560, 9728), (200, 384), (48, 128), (5120,
 def test_prefill_accesses_in_bounds(N, K, bits):
     for M in (65, 300, 512):
         prefill_accesses(N, K, M, bits)
+
+
+def store4_targets(N, nparts, offs, t, n):
+    """prefill.hip store4 restated: the (part, flat index) each of columns n .. n + 3 of token t is written to, and
+    whether the 16-byte path is taken (base pointers taken as 16-byte aligned, as det_malloc's are)."""
+    if nparts <= 1:
+        part, lo, width = 0, 0, N
+    else:
+        part, lo, hi = 0, offs[0], offs[1]
+        for j in range(1, 4):
+            if j < nparts and n >= offs[j]:
+                part, lo, hi = j, offs[j], offs[j + 1]
+        width = hi - lo
+    vec = n - lo + 4 <= width and (n - lo) % 4 == 0 and width % 4 == 0
+    if vec:
+        return [(part, t * width + (n - lo) + e) for e in range(4)], True
+    out = []
+    for e in range(4):                      # the scalar path routes each column on its own (Out::ptr)
+        c = n + e
+        if c >= N:
+            continue
+        if nparts <= 1:
+            out.append((0, t * N + c))
+            continue
+        p, l, h = 0, offs[0], offs[1]
+        for j in range(1, 4):
+            if j < nparts and c >= offs[j]:
+                p, l, h = j, offs[j], offs[j + 1]
+        out.append((p, t * (h - l) + (c - l)))
+    return out, False
+
+
+@pytest.mark.parametrize('widths', [(256,), (200,), (130, 126), (100, 36, 164), (8192, 1024, 1024), (32, 32),
+                                    (3, 5, 7, 9), (1024, 3)])
+def test_epilogue_routing(widths):
+    """Every column of every token is written exactly once, into the part GemmOut::Parts assigns it
+    (backend.rs:138-142: column n in [offs[i], offs[i+1]) goes to dst[i][t][n - offs[i]]), inside that part."""
+    N = sum(widths)
+    nparts = len(widths)
+    offs = list(np.cumsum([0] + list(widths))) + [0] * (5 - nparts - 1)
+    M = 3
+    hits = {}
+    for t in range(M):
+        for n0 in range(0, ((N + 127) // 128) * 128, 32):           # wave slabs of 32 rows
+            for c4 in range(0, 32, 4):
+                n = n0 + c4
+                if n >= N:
+                    continue
+                tg, _ = store4_targets(N, nparts, offs, t, n)
+                for tgt in tg:
+                    hits[tgt] = hits.get(tgt, 0) + 1
+    want = {}
+    for t in range(M):
+        for c in range(N):
+            if nparts <= 1:
+                want[(0, t * N + c)] = 1
+            else:
+                i = max(j for j in range(nparts) if c >= offs[j])
+                want[(i, t * widths[i] + c - offs[i])] = 1
+    assert hits == want
