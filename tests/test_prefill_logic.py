@@ -238,3 +238,43 @@ def test_epilogue_routing(widths):
                 i = max(j for j in range(nparts) if c >= offs[j])
                 want[(i, t * widths[i] + c - offs[i])] = 1
     assert hits == want
+
+
+GB = {8: 128, 6: 96, 4: 64}          # packed bytes of one 128-group
+BPL = {8: 32, 6: 24, 4: 16}          # packed bytes of one 32-code block
+
+
+@pytest.mark.parametrize('bits', [4, 6, 8])
+@pytest.mark.parametrize('N,K', SHAPES + [(248320, 2560), (1, 128), (129, 256), (4097, 384)])
+def test_repack_writes_in_bounds(N, K, bits):
+    """det_linear_repack's two kernels, restated at the extremes of their index ranges: k_repack (decode tiles, c, m)
+    and k_repack_pf (prefill planes) write only inside the wq / c / m sizes det_linear_sizes reports, the two wq
+    regions are disjoint and together cover wq exactly, and rows are read only for n < N."""
+    import os
+    from det_amd import ffi
+    if not os.path.exists(ffi.LIB_PATH):
+        pytest.skip('libdet_hip.so not built')
+    wq_bytes, c_bytes, m_bytes = ffi.linear_sizes(N, K, bits)
+    G = K // GROUP
+    T = 2 * ((N + 127) // 128)                              # 64-row tiles, whole pairs
+    pf_offset = T * G * GB[bits] * 64                       # prefill.hip pf_offset
+    rb = K // 32 * BPL[bits] + 4 + 2 * G
+    # k_repack: idx < nchunks = pf_offset / 16; lane r = idx % 64, chunk c, group g, tile
+    nchunks = pf_offset // 16                               # (wq_bytes / 16 would overrun m and c)
+    NC = GB[bits] // 16
+    last = nchunks - 1
+    assert 16 * last + 16 == pf_offset <= wq_bytes
+    tg_max = (last >> 6) // NC
+    assert (tg_max * 64 + 63) * 2 + 2 <= m_bytes                       # ms[tg * 64 + r]
+    tile_max = tg_max // G
+    assert (tile_max * 64 + 63) * 4 + 4 <= c_bytes                      # cs[n], n = tile * 64 + r
+    n_read = min(tile_max * 64 + 63, N - 1)                             # rows read only for n < N
+    assert n_read * rb + (G - 1) * GB[bits] + (NC - 1) * 16 + 16 <= N * rb
+    assert n_read * rb + K // 32 * BPL[bits] + 6 + 2 * (G - 1) <= N * rb
+    # k_repack_pf: items = 4 ceil(N / 128) G 64; block-group bg = idx / 64, lane l; writes dst[p * 64] for p < NP
+    items = 4 * ((N + 127) // 128) * G * 64
+    bg_max = (items - 1) >> 6
+    hi = pf_offset + bg_max * NP[bits] * 1024 + 63 * 16 + (NP[bits] - 1) * 1024 + 16
+    assert hi == wq_bytes, (hi, wq_bytes)
+    # both kernels together write every byte of wq exactly once: the regions abut and have the sizes written above
+    assert nchunks * 16 + items // 64 * NP[bits] * 1024 == wq_bytes
