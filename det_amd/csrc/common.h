@@ -27,6 +27,9 @@ constexpr int TILE_N = 64;
 // staying dirty in one XCD's L2; this wait blocks until every memory operation of the wave has been performed, and
 // the memory clobber keeps the compiler from moving loads or stores across it.  Only then is the arrival counter
 // bumped, and the consumer that sees the final count reads with agent-scope atomic loads.
+// This is an ordering by completion, not a release/acquire pair of the language's memory model: on gfx950 an
+// agent-scope release compiles to an L2 write-back (buffer_wbl2) and an acquire to an L2 invalidate, which measured
+// tens of microseconds per split-K call, while every value handed over here is itself an agent-scope atomic.
 __device__ __forceinline__ void wait_performed() { asm volatile("s_waitcnt 0" ::: "memory"); }
 
 __device__ __forceinline__ float fmax_spec(float a, float b) {   // spec/prim.rs:58-70 (-0 below +0, NaN wins)
