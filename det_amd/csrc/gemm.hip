@@ -410,7 +410,7 @@ __global__ void __launch_bounds__(128 * DMS_MAXP) k_decode_ms(const uint8_t* __r
             for (int r = 0; r < 16; r++) {
                 // d4 < 2^9, d3 < 2^15, d2, d1 < 2^20, d0 < 2^19 (32 slots): S = hi 2^14 + lo with
                 // hi = (d4 2^7 + d3) 2^7 + d2 < 2^25 and lo = d1 2^7 + d0 < 2^28, one v_mad_u64_u32
-                const uint32_t hi = (((uint32_t)d4[r] << 7) + (uint32_t)d3[r] << 7) + (uint32_t)d2[r];
+                const uint32_t hi = ((((uint32_t)d4[r] << 7) + (uint32_t)d3[r]) << 7) + (uint32_t)d2[r];
                 const uint32_t lo = ((uint32_t)d1[r] << 7) + (uint32_t)d0[r];
                 const unsigned long long S = (unsigned long long)hi * 16384u + lo;
                 U[t][r] -= S << 21;
