@@ -106,15 +106,16 @@ template <> __device__ __forceinline__ void block_unsigned<8>(const uint32_t* q,
 // Global -> LDS copy by the buffer unit (BYTES = 4 or 16 per lane, lane i's bytes land at lds + i * BYTES), written as
 // inline assembly so that the compiler does not track it: with the builtin it cannot tell that later LDS reads touch
 // other buffers and waits for every copy in flight before the first of them.  The caller waits (s_waitcnt vmcnt)
-// and synchronises before reading the target.  `lds` must be wave-uniform.
+// and synchronises before reading the target.  `lds` must be wave-uniform; it travels in M0, which the asm takes as
+// an operand (constraint {m0}), so that the compiler sets M0 itself and knows its value around every copy.
 template <int BYTES>
 __device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff_, const void* lds) {
     const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
     const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
     if (BYTES == 16)
-        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
+        asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
     else
-        asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "s"(m0v) : "memory", "m0");
+        asm volatile("buffer_load_dword %0, %1, %2 offen lds" :: "v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
 }
 
 // N (<= 4) copies of 16 bytes per lane under one M0 value: copy i reads the resource at voff[i] + soff + 1024 i and
@@ -126,38 +127,33 @@ __device__ __forceinline__ void dma16_run(__amdgpu_buffer_rsrc_t r, const uint32
     const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
     static_assert(N >= 1 && N <= 4, "at most 4 copies per run");
     if constexpr (N == 4)
-        asm volatile("s_mov_b32 m0, %5\n\t"
-                     "buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
+        asm volatile("buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
                      "buffer_load_dwordx4 %1, %4, %6 offen offset:1024 lds\n\t"
                      "buffer_load_dwordx4 %2, %4, %6 offen offset:2048 lds\n\t"
                      "buffer_load_dwordx4 %3, %4, %6 offen offset:3072 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "{m0}"(m0v), "s"(soff) : "memory");
     else if constexpr (N == 3)
-        asm volatile("s_mov_b32 m0, %4\n\t"
-                     "buffer_load_dwordx4 %0, %3, %5 offen lds\n\t"
+        asm volatile("buffer_load_dwordx4 %0, %3, %5 offen lds\n\t"
                      "buffer_load_dwordx4 %1, %3, %5 offen offset:1024 lds\n\t"
                      "buffer_load_dwordx4 %2, %3, %5 offen offset:2048 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+                     :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "s"(r), "{m0}"(m0v), "s"(soff) : "memory");
     else if constexpr (N == 2)
-        asm volatile("s_mov_b32 m0, %3\n\t"
-                     "buffer_load_dwordx4 %0, %2, %4 offen lds\n\t"
+        asm volatile("buffer_load_dwordx4 %0, %2, %4 offen lds\n\t"
                      "buffer_load_dwordx4 %1, %2, %4 offen offset:1024 lds"
-                     :: "v"(voff[0]), "v"(voff[1]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+                     :: "v"(voff[0]), "v"(voff[1]), "s"(r), "{m0}"(m0v), "s"(soff) : "memory");
     else
-        asm volatile("s_mov_b32 m0, %2\n\t"
-                     "buffer_load_dwordx4 %0, %1, %3 offen lds"
-                     :: "v"(voff[0]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+        asm volatile("buffer_load_dwordx4 %0, %1, %3 offen lds"
+                     :: "v"(voff[0]), "s"(r), "{m0}"(m0v), "s"(soff) : "memory");
 }
 // four copies under one M0 through one resource, copy i at voff[i] + soff + 1024 i, landing at lds + 1024 i + 16 lane
 __device__ __forceinline__ void dma16_run4v(__amdgpu_buffer_rsrc_t r, const uint32_t* voff, uint32_t soff_, const void* lds) {
     const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
     const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    asm volatile("s_mov_b32 m0, %5\n\t"
-                 "buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
+    asm volatile("buffer_load_dwordx4 %0, %4, %6 offen lds\n\t"
                  "buffer_load_dwordx4 %1, %4, %6 offen offset:1024 lds\n\t"
                  "buffer_load_dwordx4 %2, %4, %6 offen offset:2048 lds\n\t"
                  "buffer_load_dwordx4 %3, %4, %6 offen offset:3072 lds"
-                 :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "s"(m0v), "s"(soff) : "memory", "m0");
+                 :: "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), "s"(r), "{m0}"(m0v), "s"(soff) : "memory");
 }
 // four copies under one M0, copy i through resource r[i] at voff[i % 2] + soff + 1024 i, landing at
 // lds + 1024 i + 16 lane
@@ -165,12 +161,11 @@ __device__ __forceinline__ void dma16_run4x(const __amdgpu_buffer_rsrc_t* r, uin
                                             const void* lds) {
     const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_);
     const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds);
-    asm volatile("s_mov_b32 m0, %6\n\t"
-                 "buffer_load_dwordx4 %0, %2, %7 offen lds\n\t"
+    asm volatile("buffer_load_dwordx4 %0, %2, %7 offen lds\n\t"
                  "buffer_load_dwordx4 %1, %3, %7 offen offset:1024 lds\n\t"
                  "buffer_load_dwordx4 %0, %4, %7 offen offset:2048 lds\n\t"
                  "buffer_load_dwordx4 %1, %5, %7 offen offset:3072 lds"
-                 :: "v"(voff0), "v"(voff1), "s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[3]), "s"(m0v), "s"(soff) : "memory", "m0");
+                 :: "v"(voff0), "v"(voff1), "s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[3]), "{m0}"(m0v), "s"(soff) : "memory");
 }
 
 

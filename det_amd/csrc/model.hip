@@ -66,7 +66,7 @@ struct det_model {
     std::vector<float> host_x;
 
     ~det_model() {
-        if (st) hipStreamSynchronize(st);
+        if (st) (void)hipStreamSynchronize(st);     // teardown: a device error was reported where it happened
         for (void* p : allocs) det_free(p);
     }
     template <class T> T* alloc(size_t n) {
@@ -121,7 +121,8 @@ struct det_model {
         float* cs = alloc<float>(cb / 4);
         uint16_t* ms = alloc<uint16_t>(mb / 2);
         det_linear_repack(static_cast<const uint8_t*>(rows), (int)N, (int)K, bits, wq, cs, ms, st);
-        hipStreamSynchronize(st);
+        const hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) throw Error(std::string("weight repack failed on the device: ") + hipGetErrorString(e));
         det_free(rows);
         L.q = det_qlinear{wq, cs, ms, (int)N, (int)K, bits};
         return L;
