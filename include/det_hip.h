@@ -19,11 +19,11 @@ extern "C" {
 // ---- runtime (replaces kernels/cuda/runtime.cu; declarations of det_cuda.h:15-24)
 int         det_init(void);                 // selects the current device; 0 on success (called lazily otherwise)
 const char* det_device_name(void);
-void*       det_malloc(size_t bytes);       // zero-initialised device buffer; NULL on failure
+void*       det_malloc(size_t bytes);       // a device block filled with zero bytes, or NULL when none is available
 void        det_free(void* p);              // waits for pending work first; aborts on a pointer det_malloc did not return
 size_t      det_allocated_bytes(void);
-void        det_sync(void);                 // wait for all pending GPU work (aborts on a kernel error)
-void        det_flush(void);                // no-op (launches are already submitted)
+void        det_sync(void);                 // returns once the device is idle; a failed kernel ends the process
+void        det_flush(void);                // nothing to do: every launch reaches the device when it is made
 void        det_memset(void* p, int value, size_t bytes, hipStream_t st);
 void        det_memcpy(void* dst, const void* src, size_t bytes, hipStream_t st);   // any direction (hipMemcpyDefault)
 void*       det_hip_stream(void);           // the stream det's work runs on (det_cuda_stream, det_cuda.h:24)
@@ -43,7 +43,7 @@ typedef struct {
     const uint8_t* wq;
     const float*   c;
     const uint16_t* m;
-    int N, K, bits;      // bits in {4,6,8}
+    int N, K, bits;      // bits: 4, 6 or 8
 } det_qlinear;
 
 // Sizes of the three planes of det_linear_repack for an N x K linear of `bits`.
@@ -59,20 +59,24 @@ void det_linear_repack(const uint8_t* rows, int N, int K, int bits, uint8_t* wq,
 void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hipStream_t st);
 
 // ---- glue (replaces kernels/cuda/norm.cu; det_cuda.h:35-42)
-// Activation quantization (spec quant_act_i8g): per row sx[M] fp32 and, if mx != NULL, per-(row, 128-group)
-// multipliers mx[M][n/128] uint16 (n must be a multiple of 128); if mx == NULL, plain per-row int8 (quant_act_i8).
+// x[M][n] -> int8 codes xq[M][n] with one fp32 scale per row, sx[M].  Given mx, also one uint16 multiplier per row
+// and 128-column group, mx[M][n/128] (then n % 128 == 0): the spec's quant_act_i8g.  mx == NULL: the per-row form
+// quant_act_i8.
 void det_quant(const float* x, int M, int n, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st);
-// x[M][n] -> y[M][n] = rmsnorm(x,w,eps) (y may be NULL) and, if xq != NULL, quantize y into xq[M][n], sx, mx
+// RMS-normalise each row of x[M][n] with weights w and eps into y (skipped when y is NULL); when xq is given, the
+// normalised rows are also quantized as det_quant does.
 void det_rmsnorm_quant(const float* x, const float* w, float eps, int M, int n, float* y, int8_t* xq, float* sx, uint16_t* mx, hipStream_t st);
-// h = silu(g)*u (h may be NULL) + quant
+// silu(g) * u per element into h (skipped when h is NULL), then quantized into hq, sh, mh as det_quant does.
 void det_silu_mul_quant(const float* g, const float* u, int M, int n, float* h, int8_t* hq, float* sh, uint16_t* mh, hipStream_t st);
 
 // ---- GEMM (replaces kernels/cuda/gemm.cu; det_cuda.h:45-57)
-//      y[M][N] = ((float)acc * c[n]) * sx[m],  acc = sum_g (m[n,g]*mx[m,g]) * sum_{k in g} wq[n,k]*xq[m,k]
-//      mx[M][K/128] uint16 (NULL = all ones).  acc exact in int64.  accumulate != 0: y += result.  nparts > 1: the
-//      output columns are routed into nparts buffers (part i = columns [offs[i], offs[i+1]), offs[0] == 0, dsts[i] is
-//      [M][width_i]; y unused).  M < 1 is a no-op.  K % 128 != 0, N < 1, nparts > 4, offs[0] != 0, y == NULL
-//      (with nparts <= 1) or bits not in {4,6,8}: message on stderr and abort().
+// For token t and output row n: acc = sum over 128-groups g of m[n][g] * mx[t][g] * (the integer dot product of
+// the codes of row n and of token t within g), computed exactly in int64; mx == NULL means every mx is 1.  The
+// result is ((float)acc * c[n]) * sx[t], written to y[t][n], or added to it when accumulate is nonzero.  With
+// nparts from 2 to 4, the columns are split instead: columns offs[i] .. offs[i+1] - 1 go to dsts[i], a
+// [M][offs[i+1] - offs[i]] array (offs[0] must be 0; y is ignored).  M < 1 does nothing.  Aborts with a message for
+// K not a multiple of 128, N < 1, more than 4 parts, offs[0] != 0, a NULL y with one part, or bits other than
+// 4, 6, 8.
 void det_gemm(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, hipStream_t st);
 void det_gemm_ex(const det_qlinear* L, const int8_t* xq, const float* sx, const uint16_t* mx, int M, float* y, int accumulate,
                  int nparts, const int* offs, float* const* dsts, hipStream_t st);
@@ -123,9 +127,11 @@ void det_argmax(const float* logits, int M, int V, int* out, hipStream_t st);
 
 // ---- test hooks (det_test_prim of runtime.cu; det_cuda.h:114-118): the spec's fp32 primitives applied to an array,
 // so that tests can compare them bit for bit with the spec.
-// op: 0 exp_f, 1 log_f, 2 softplus_f, 3 sigmoid_f, 4 silu_f, 5 i64->f32 of (long long) bits of x pairs (x[2i],x[2i+1]),
-//     6 rint, 7 1/x, 8 sqrt, 9 x*y (y = x reversed), 10 x+y, 11 treesum of each row of n (out[M]), 12 native i64->f32,
-//     13 rint as int, 14 x/y, 15 x-y, 16 max(x,y)
+// Ops by number.  One operand, element by element: exp_f 0, log_f 1, softplus_f 2, sigmoid_f 3, silu_f 4, rint 6,
+// reciprocal 7, square root 8, rint then saturating conversion to int32 (stored as fp32) 13.  Two operands,
+// element i with element M n - 1 - i: product 9, sum 10, quotient 14, difference 15, spec maximum 16.  Pairs
+// (x[2i] low bits, x[2i+1] high bits) read as one int64 and converted to fp32 into out[2i]: by the spec's
+// rounding 5, by the compiler's conversion 12.  The spec's pairwise tree sum of each row of n into out[row]: 11.
 void det_test_prim(int op, const float* x, int M, int n, float* out, hipStream_t st);
 // Test hooks of the model runner's one-token FFN path (no det_cuda.h counterpart; for tests of this library):
 //   det_test_gemv_silu0: det_gemm_ex with M = 1 and Parts output (2 to 4 parts from column 0), storing silu_f(v)
