@@ -109,8 +109,16 @@ __global__ void k_repack_pf(const uint8_t* __restrict__ rows, int N, int K, int 
 // the MFMA A operands of the four 32-k steps from a lane's prefill words (codes scaled by 2^SH)
 template <int BITS> __device__ __forceinline__ void pf_unpack(const v4i* q, v4i* a);
 template <> __device__ __forceinline__ void pf_unpack<8>(const v4i* q, v4i* a) {
+    // the codes are the operands; copied by asm (the next group's loads reuse q while the MFMAs read a), so that the
+    // copy stays behind the wait, which a plain assignment the compiler could place anywhere would not
+    typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int s = 0; s < 4; s++) a[s] = q[s];
+    for (int s = 0; s < 4; s++) {
+        const u64x2 in = __builtin_bit_cast(u64x2, q[s]);
+        unsigned long long lo, hi;
+        asm volatile("v_mov_b64 %0, %2\n\tv_mov_b64 %1, %3" : "=v"(lo), "=v"(hi) : "v"(in.x), "v"(in.y));
+        a[s] = __builtin_bit_cast(v4i, u64x2{lo, hi});
+    }
 }
 template <> __device__ __forceinline__ void pf_unpack<6>(const v4i* q, v4i* a) {
     const uint32_t* w = reinterpret_cast<const uint32_t*>(q);
@@ -145,7 +153,11 @@ __device__ __forceinline__ void ld16(v4i& d, __amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ void ld_u16(uint32_t& d, __amdgpu_buffer_rsrc_t r, uint32_t voff) {
     asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(d) : "v"(voff), "s"(r) : "memory");
 }
-// wait until at most KEEP vector-memory operations of this wave are outstanding
+// wait until at most KEEP vector-memory operations of this wave are outstanding, then hand the loaded registers to
+// the code that follows: the asm claims to modify them, so no use of them can move above the wait.  This holds only
+// if the registers reach the asm where the loads put them (a copy placed before the asm would read them early):
+// every iteration of the group loop issues the same loads and waits the same way, so that no path merges loaded and
+// not-loaded values, and tests/test_isa_waits.py proves it on the generated code.
 template <int NP, int KEEP>
 __device__ __forceinline__ void pf_wait(v4i* q, uint32_t& s) {
     if constexpr (NP == 4)
@@ -155,6 +167,7 @@ __device__ __forceinline__ void pf_wait(v4i* q, uint32_t& s) {
     else
         asm volatile("s_waitcnt vmcnt(%3)" : "+v"(q[0]), "+v"(q[1]), "+v"(s) : "i"(KEEP) : "memory");
 }
+__device__ __forceinline__ void pf_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // store four consecutive outputs (columns n .. n + 3 of token t) through the output routing
 __device__ __forceinline__ void store4(const Out& out, int N, int M, int t, int n, const float4& v) {
@@ -203,9 +216,11 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                                                      unsigned int* __restrict__ cnt) {
     constexpr int NP = pf_planes<BITS>(), SH = pf_shift<BITS>();
     __shared__ __attribute__((aligned(16))) int8_t As[PF_STG][PF_BM * 128];
-    __shared__ __attribute__((aligned(16))) uint32_t mv_s[2][PF_BN];        // m of the tile's rows, by group parity
-    __shared__ __attribute__((aligned(16))) uint32_t xv_s[2][PF_BM];        // mx of the tile's tokens
-    __shared__ __attribute__((aligned(16))) uint8_t dig[2][3][128][PF_SLOTS];   // 7-bit digits: [0] m (rows), [1] mx (tokens)
+    // multipliers by group parity: entries 0-127 m of the tile's rows, 128-255 mx of its tokens; thread tid stages
+    // entry tid, so its slot address is a function of tid alone (no per-thread base register to keep alive)
+    __shared__ __attribute__((aligned(16))) uint32_t sv_s[2][PF_BN + PF_BM];
+    // their 7-bit digits for the bias removal, [digit][entry as in sv_s][group slot]
+    __shared__ __attribute__((aligned(16))) uint8_t dig[3][PF_BN + PF_BM][PF_SLOTS];
     __shared__ unsigned int last_s;
 
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
@@ -231,7 +246,7 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         ? __builtin_amdgcn_make_buffer_rsrc((void*)ms, (short)0, nbn * 2 * G * 128, 0x00020000)
         : __builtin_amdgcn_make_buffer_rsrc((void*)(mx ? mx : ms), (short)0, mx ? M * G * 2 : 0, 0x00020000);
     const uint32_t sstride = is_m ? 128u : 2u;
-    uint8_t* const dg = &dig[is_m ? 0 : 1][0][sidx][0];      // this thread's digit slots (planes 4 KB apart)
+    uint8_t* const dg = &dig[0][tid][0];                      // this thread's digit slots (planes 8 KB apart)
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, M * K, 0x00020000);
     // LDS byte offsets of this lane's B operands: token l32 (+ 32 j), chunk 2 s + h of the group
     uint32_t boff[4];
@@ -283,55 +298,53 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
         uint32_t sreg = 0;
         auto issue_s = [&](int g) __attribute__((always_inline)) { ld_u16(sreg, sres, s_vo + (uint32_t)g * sstride); };
 
-        // prologue: group ga's multiplier into LDS; copies of ga (and ga + 1), codes of ga
+        // prologue: group ga's multiplier into LDS; copies of ga and ga + 1, codes of ga.  Loads are issued for
+        // every group position, the ones past the fragment's last group repeating that group (gl), so that every
+        // iteration issues and waits alike: the group's wait always leaves exactly the newest four copies in flight.
+        const int gl = gb - 1;
         issue_s(ga);
         pf_wait<NP, 0>(qn, sreg);
         uint32_t scur = x_one ? 1u : sreg;
-        (is_m ? mv_s[0] : xv_s[0])[sidx] = scur;
+        sv_s[0][tid] = scur;
         issue_a(ga, 0);
         issue_w(ga);
-        if (ga + 1 < gb) {
-            issue_s(ga + 1);
-            issue_a(ga + 1, 1);
-        }
+        issue_s(std::min(ga + 1, gl));
+        issue_a(std::min(ga + 1, gl), 1);
 
         int stg = 0;
         for (int i = 0, g = ga; g < gb; i++, g++) {
             const int par = i & 1;
             // this group's copies, codes and the next group's multiplier have landed (the next group's copies may
             // still be in flight: they are the last four operations issued)
-            if (g + 1 < gb) pf_wait<NP, 4>(qn, sreg);
-            else pf_wait<NP, 0>(qn, sreg);
+            pf_wait<NP, 4>(qn, sreg);
             __syncthreads();                      // ... in every wave; and group g - 1's readers are done
             const uint32_t snext = x_one ? 1u : sreg;
-            if (g + 1 < gb) (is_m ? mv_s[par ^ 1] : xv_s[par ^ 1])[sidx] = snext;
+            if (g + 1 < gb) sv_s[par ^ 1][tid] = snext;
             const int slot = i & (PF_SLOTS - 1);
             if (slot == 0 && gb - g < PF_SLOTS) {  // a short last batch: clear this thread's slots
 #pragma unroll
                 for (int d = 0; d < 3; d++) {
-                    uint4* p = reinterpret_cast<uint4*>(dg + d * 128 * PF_SLOTS);
+                    uint4* p = reinterpret_cast<uint4*>(dg + d * (PF_BN + PF_BM) * PF_SLOTS);
                     p[0] = make_uint4(0, 0, 0, 0);
                     p[1] = make_uint4(0, 0, 0, 0);
                 }
             }
             dg[slot] = (uint8_t)(scur & 127);
-            dg[128 * PF_SLOTS + slot] = (uint8_t)((scur >> 7) & 127);
-            dg[2 * 128 * PF_SLOTS + slot] = (uint8_t)(scur >> 14);
+            dg[(PF_BN + PF_BM) * PF_SLOTS + slot] = (uint8_t)((scur >> 7) & 127);
+            dg[2 * (PF_BN + PF_BM) * PF_SLOTS + slot] = (uint8_t)(scur >> 14);
             scur = snext;
 
             v4i a[4];
             pf_unpack<BITS>(qn, a);
             // loads for the next groups, the copies last (the wait above keeps exactly those in flight)
-            if (g + 1 < gb) issue_w(g + 1);
-            if (g + 2 < gb) {
-                issue_s(g + 2);
-                issue_a(g + 2, stg == 0 ? 2 : stg - 1);
-            }
+            issue_w(std::min(g + 1, gl));
+            issue_s(std::min(g + 2, gl));
+            issue_a(std::min(g + 2, gl), stg == 0 ? 2 : stg - 1);     // the stage group g - 1 used
 
             const int8_t* Ab = As[stg];
             uint32_t xm[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) xm[j] = xv_s[par][32 * j + l32];
+            for (int j = 0; j < 4; j++) xm[j] = sv_s[par][PF_BN + 32 * j + l32];
 #pragma unroll
             for (int p = 0; p < 2; p++) {
                 v16i d0 = biasv, d1 = biasv;
@@ -345,7 +358,7 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                 // element (row, token): lane = token, register 4 (row / 8) + row % 4 with (row / 4) % 2 = h
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
-                    const uint4 mq = *reinterpret_cast<const uint4*>(&mv_s[par][wv * 32 + 8 * q4 + 4 * h]);
+                    const uint4 mq = *reinterpret_cast<const uint4*>(&sv_s[par][wv * 32 + 8 * q4 + 4 * h]);
                     const uint32_t mvv[4] = {mq.x, mq.y, mq.z, mq.w};
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
@@ -361,12 +374,12 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                 __syncthreads();                  // every thread's digits of this batch are in LDS
                 v4i Ad[3];
 #pragma unroll
-                for (int d = 0; d < 3; d++) Ad[d] = *reinterpret_cast<const v4i*>(&dig[0][d][wv * 32 + l32][16 * h]);
+                for (int d = 0; d < 3; d++) Ad[d] = *reinterpret_cast<const v4i*>(&dig[d][wv * 32 + l32][16 * h]);
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     v4i Bd[3];
 #pragma unroll
-                    for (int d = 0; d < 3; d++) Bd[d] = *reinterpret_cast<const v4i*>(&dig[1][d][32 * j + l32][16 * h]);
+                    for (int d = 0; d < 3; d++) Bd[d] = *reinterpret_cast<const v4i*>(&dig[d][PF_BN + 32 * j + l32][16 * h]);
                     const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
                     // digit weights 2^28 (sum < 2^9), 2^21 (< 2^15), 2^14 (< 2^21), 2^7 (< 2^20): t stays below 2^32
                     v16i t = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ad[2], Bd[2], z, 0, 0, 0);
@@ -392,6 +405,11 @@ __global__ void __launch_bounds__(256, 2) k_prefill(const uint8_t* __restrict__ 
                 }
             }
         }
+
+        // the repeated loads of the last two iterations: their registers and LDS stage are free for reuse only once
+        // they have landed, in every wave
+        pf_drain();
+        __syncthreads();
 
         // ---- a tile split between workgroups: every fragment but the last to arrive stores its exact partial
         // (agent-scope stores: coherent across the XCDs' L2s) and counts itself; the last adds the others

@@ -88,7 +88,7 @@ def emulate(rows, N, K, bits, xq, sx, mx, cus, P=None):
         nb, tb = divmod(tile, nbt)
         t0, n0 = tb * 128, nb * 128
         U = np.zeros((4, 4, 64, 16), np.uint64)          # [wave][t-block][lane][register]
-        dig = np.zeros((2, 3, 128, 32), np.int64)
+        dig = np.zeros((3, 256, 32), np.int64)           # [digit][entry: rows 0-127, tokens 128-255][slot]
         for i, g in enumerate(range(ga, gb)):
             slot = i % 32
             if slot == 0 and gb - g < 32:
@@ -106,14 +106,14 @@ def emulate(rows, N, K, bits, xq, sx, mx, cus, P=None):
             mv = np.array([mrow[n0 + s, g] for s in range(128)], np.int64)
             xv = np.array([(int(mx[t0 + s, g]) if t0 + s < M else 0) if mx is not None else 1 for s in range(128)],
                           np.int64)
-            for s in range(128):
+            sv = np.concatenate([mv, xv])                    # sv_s[par]: thread tid stages entry tid
+            for e in range(256):
                 for d in range(3):
-                    dig[0, d, s, slot] = (mv[s] >> (7 * d)) & 127 if d < 2 else mv[s] >> 14
-                    dig[1, d, s, slot] = (xv[s] >> (7 * d)) & 127 if d < 2 else xv[s] >> 14
+                    dig[d, e, slot] = (sv[e] >> (7 * d)) & 127 if d < 2 else sv[e] >> 14
             boff = [np.array([swz(int(l32[l]), 2 * s + int(h[l])) for l in range(64)]) for s in range(4)]
             for wv in range(4):
                 a = np.stack([pf_unpack(words[nb * 4 + wv, g, l], bits) for l in range(64)])   # [64][64] k order
-                xm = [xv[32 * j + l32] for j in range(4)]
+                xm = [sv[128 + 32 * j + l32] for j in range(4)]
                 for p in range(2):
                     d0 = np.full((64, 16), BIAS, np.int64)
                     d1 = np.full((64, 16), BIAS, np.int64)
@@ -126,17 +126,17 @@ def emulate(rows, N, K, bits, xq, sx, mx, cus, P=None):
                     for q4 in range(4):
                         for e in range(4):
                             r = 4 * q4 + e
-                            mvv = mv[wv * 32 + 8 * q4 + 4 * h + e]
+                            mvv = sv[wv * 32 + 8 * q4 + 4 * h + e]
                             for jj, dd in ((2 * p, d0), (2 * p + 1, d1)):
                                 assert (dd[:, r] >= 0).all(), 'biased partial negative'
                                 prod = (dd[:, r].astype(np.uint64) * (mvv * xm[jj]).astype(np.uint64))
                                 U[wv, jj, :, r] = U[wv, jj, :, r] + prod
             if slot == 31 or g + 1 == gb:
                 for wv in range(4):
-                    Ad = [np.stack([dig[0, d, wv * 32 + l32[l], 16 * h[l]:16 * h[l] + 16] for l in range(64)])
+                    Ad = [np.stack([dig[d, wv * 32 + l32[l], 16 * h[l]:16 * h[l] + 16] for l in range(64)])
                           for d in range(3)]
                     for j in range(4):
-                        Bd = [np.stack([dig[1, d, 32 * j + l32[l], 16 * h[l]:16 * h[l] + 16] for l in range(64)])
+                        Bd = [np.stack([dig[d, 128 + 32 * j + l32[l], 16 * h[l]:16 * h[l] + 16] for l in range(64)])
                               for d in range(3)]
                         z = np.zeros((64, 16), np.int64)
                         S = np.zeros((64, 16), object)
