@@ -27,6 +27,19 @@ BRANCH = re.compile(r'^s_(c?branch)\w*$')
 CAP = 63            # the counter's capacity: an operation with 63 newer ones has completed
 
 
+_CACHE = {}
+
+
+def asm_of(source):
+    """compile_asm into a scratch directory, once per source and modification time in this process."""
+    import tempfile
+    key = (os.path.abspath(source), os.path.getmtime(source))
+    if key not in _CACHE:
+        d = tempfile.mkdtemp(prefix='det_asm_')
+        _CACHE[key] = compile_asm(source, os.path.join(d, os.path.basename(source) + '.s'))
+    return _CACHE[key]
+
+
 def compile_asm(source, out_path):
     """The device assembly of one source file, built with the library's flags (det_amd/build.py).  The source is
     compiled to an object (so that the assembler validates every instruction, inline assembly included) and the

@@ -1,0 +1,262 @@
+"""The compiled GEMM kernels, run instruction by instruction on the CPU (tests/gfx950_emu.py) and compared bit for bit
+with the oracle.
+
+This covers what the lane-level restatement (tests/test_prefill_emulation.py) cannot: the code hipcc actually
+generated for gfx950 -- register allocation, the inline-assembly loads and their waits, the buffer-unit copies into
+LDS, scalar address arithmetic, spills -- for the load-time repack (k_repack, k_repack_pf) and both prefill kernels.
+The emulator keeps every vector-memory load and LDS copy pending until the wave's `s_waitcnt` retires it and fails on
+any earlier use, so a missing wait fails here instead of giving wrong results on a GPU.  k_prefill2, which has run
+on MI355X and matched the oracle there, is run too: it checks the emulator against the hardware's behaviour.
+
+The host launch logic is restated from det_amd/csrc (launch_prefill, launch_prefill2, det_linear_repack): grid
+sizes, K-slices, the persistent grid and the partial-tile buffers, with `cus` chosen small so that the stream-K
+kernel splits tiles between workgroups.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import gfx950_emu as E
+from tests import isa_waits
+from tests.helpers import same_f32
+from tests.test_prefill_emulation import build_planes
+
+GROUP = 128
+BPL = {8: 32, 6: 24, 4: 16}
+NP = {8: 4, 6: 3, 4: 2}
+HIPCC = os.path.join(os.environ.get('ROCM_PATH', '/opt/rocm'), 'bin', 'hipcc')
+pytestmark = pytest.mark.skipif(not os.path.exists(HIPCC), reason='hipcc not available')
+
+
+@pytest.fixture(scope='module')
+def asm():
+    return {src: isa_waits.asm_of(os.path.join(isa_waits.CSRC, src)) for src in ('gemm.hip', 'prefill.hip')}
+
+
+def sizes(N, K, bits):
+    T, G = 2 * ((N + 127) // 128), K // GROUP
+    gb = 4 * BPL[bits]
+    return T, G, 2 * T * G * gb * 64, T * 64 * 4, T * G * 64 * 2
+
+
+def out_struct(y, nparts=1, offs=(0, 0, 0, 0, 0), dsts=(0, 0, 0, 0), acc=0):
+    b = y.to_bytes(8, 'little') + acc.to_bytes(4, 'little') + nparts.to_bytes(4, 'little')
+    b += b''.join(int(o).to_bytes(4, 'little', signed=True) for o in offs) + bytes(4)
+    b += b''.join(int(d).to_bytes(8, 'little') for d in dsts)
+    assert len(b) == 72
+    return b
+
+
+def repack(asm, mem, rows, N, K, bits):
+    """det_linear_repack: k_repack over the decode tiles, then k_repack_pf over the prefill planes."""
+    T, G, wq_bytes, c_bytes, m_bytes = sizes(N, K, bits)
+    rows_d = mem.alloc(rows.nbytes, rows)
+    wq, c, m = mem.alloc(wq_bytes), mem.alloc(c_bytes), mem.alloc(m_bytes)
+    pf_off = wq_bytes // 2
+    nchunks = pf_off // 16
+    p = E.Program(asm['gemm.hip'], 'k_repackEPKhiiiPhPfPtm')
+    E.launch(p, mem, min((nchunks + 255) // 256, 65536), 256, p.pack_args([rows_d, N, K, bits, wq, c, m, nchunks]))
+    items = 4 * ((N + 127) // 128) * G * 64
+    p = E.Program(asm['prefill.hip'], 'k_repack_pf')
+    E.launch(p, mem, min((items + 255) // 256, 65536), 256, p.pack_args([rows_d, N, K, bits, wq + pf_off, items]))
+    return wq, c, m
+
+
+def check_layout(mem, wq, c, m, rows, N, K, bits):
+    T, G, wq_bytes, c_bytes, m_bytes = sizes(N, K, bits)
+    nc = K // 32 * BPL[bits]
+    gb = 4 * BPL[bits]
+    w = mem.array(wq, np.uint8, wq_bytes)
+    dec = w[:wq_bytes // 2].reshape(T, G, gb // 16, 64, 16)
+    for n in range(T * 64):
+        t, r = divmod(n, 64)
+        want = rows[n, :nc] if n < N else np.zeros(nc, np.uint8)
+        assert (dec[t, :, :, r, :].reshape(-1) == want).all(), f'decode tile row {n}'
+    cv = mem.array(c, np.uint32, T * 64)
+    mv = mem.array(m, np.uint16, T * G * 64).reshape(T, G, 64)
+    for n in range(N):
+        assert cv[n] == rows[n, nc:nc + 4].view(np.uint32)[0]
+        assert (mv[n // 64, :, n % 64] == rows[n, nc + 4:].view('<u2')).all()
+    words = build_planes(rows, N, K, bits)                 # [blk][g][lane][NP * 4]
+    pf = w[wq_bytes // 2:].view(np.uint32).reshape(-1, G, NP[bits], 64, 4)
+    want = words.reshape(words.shape[0], G, 64, NP[bits], 4).transpose(0, 1, 3, 2, 4)
+    assert (pf[:want.shape[0]] == want).all(), 'prefill planes'
+
+
+def acts(mem, xq, sx, mx):
+    return mem.alloc(xq.nbytes, xq), mem.alloc(sx.nbytes, sx), (mem.alloc(mx.nbytes, mx) if mx is not None else 0)
+
+
+def run_prefill2(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus):
+    wq, c, m = lin
+    nbn, nbt = (N + 63) // 64, (M + 127) // 128
+    G, tiles = K // GROUP, nbn * nbt
+    KS = 1
+    if 2 * tiles < 3 * cus:
+        KS = max(1, min((3 * cus + 2 * tiles - 1) // (2 * tiles), G // 16))
+    gs = (G + KS - 1) // KS
+    KS = (G + gs - 1) // gs
+    part = mem.alloc(KS * nbt * 128 * nbn * 64 * 8) if KS > 1 else 0
+    cnt = mem.alloc(max(tiles, 1) * 4) if KS > 1 else 0
+    y = mem.alloc(M * N * 4)
+    x_d, sx_d, mx_d = acts(mem, xq, sx, mx)
+    p = E.Program(asm['prefill.hip'], f'k_prefill2ILi{bits}E')
+    E.launch(p, mem, tiles * KS, 256,
+             p.pack_args([wq, c, m, N, K, x_d, sx_d, mx_d, M, out_struct(y), nbn, nbt, KS, part, cnt]))
+    return mem.array(y, np.float32, M * N).reshape(M, N).copy(), KS
+
+
+def run_prefill(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus):
+    wq, c, m = lin
+    G = K // GROUP
+    nbn, nbt = (N + 127) // 128, (M + 127) // 128
+    tiles = nbn * nbt
+    total = tiles * G
+    P = min(2 * cus, max(1, total // 4))
+    if P > 8:
+        P &= ~7
+    split = total % P != 0 or (total // P) % G != 0
+    part = mem.alloc(2 * P * 128 * 128 * 8 if split else 8)
+    cnt = mem.alloc(max(tiles, 1 << 12) * 4)
+    y = mem.alloc(M * N * 4)
+    x_d, sx_d, mx_d = acts(mem, xq, sx, mx)
+    pf = wq + sizes(N, K, bits)[2] // 2
+    p = E.Program(asm['prefill.hip'], f'k_prefillILi{bits}E')
+    E.launch(p, mem, P, 256, p.pack_args([pf, c, m, N, K, x_d, sx_d, mx_d, M, out_struct(y), nbt, tiles, P, part, cnt]))
+    left = mem.array(cnt, np.uint32, tiles)
+    assert (left == 0).all(), 'tile counters not reset'
+    return mem.array(y, np.float32, M * N).reshape(M, N).copy(), P, split
+
+
+@pytest.mark.parametrize('bits', [6, 4, 8])
+def test_repack_kernels(asm, bits):
+    rng = oracle.Rng(3 + bits)
+    N, K = 200, 384
+    rows = rng.fake_rows(bits, N, K)
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    check_layout(mem, *lin, rows, N, K, bits)
+
+
+@pytest.mark.parametrize('bits', [6])
+def test_prefill2_matches_oracle(asm, bits):
+    """The GPU-verified kernel under the emulator: the emulator's model against known-good code."""
+    rng = oracle.Rng(11)
+    N, K, M = 72, 384, 70
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    got, KS = run_prefill2(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus=1)
+    d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+    assert d is None, d
+
+
+@pytest.mark.parametrize('bits', [6, 4, 8])
+def test_prefill_matches_oracle(asm, bits):
+    """k_prefill with tiles split between workgroups (partial tiles, last-arriver combine) and partial token and row
+    tiles."""
+    rng = oracle.Rng(21 + bits)
+    N, K, M = 136, 640, 200                      # 2 x 2 tiles of 5 groups over 5 workgroups of 4 groups each
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    got, P, split = run_prefill(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus=3)
+    assert split and P == 5
+    d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+    assert d is None, d
+
+
+@pytest.mark.parametrize('bits,with_mx', [(6, True), (6, False), (8, True), (4, False)])
+def test_prefill_bias_batches(asm, bits, with_mx):
+    """33 groups split over 2 workgroups: one fragment crosses a full 32-group bias batch, the other ends in a short
+    batch; without mx the token multipliers are all 1 (no mx loads)."""
+    rng = oracle.Rng(40 + bits)
+    N, K, M = 40, 128 * 33, 70
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    mx = mx if with_mx else None
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    got, P, split = run_prefill(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus=1)
+    assert split and P == 2
+    d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+    assert d is None, d
+
+
+def test_prefill_xcd_remap(asm):
+    """A 16-workgroup persistent grid (a multiple of 8: logical ids remapped so that consecutive ones share an
+    XCD) over 4 tiles of 20 groups."""
+    rng = oracle.Rng(9)
+    bits, N, K, M = 6, 256, 2560, 200
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    got, P, split = run_prefill(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus=8)
+    assert P == 16 and split                     # 5 units each: every tile split between 4 workgroups
+    d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+    assert d is None, d
+
+
+def run_prefill_out(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus, out):
+    """run_prefill with a caller-built output (Parts / Accumulate)."""
+    wq, c, m = lin
+    G = K // GROUP
+    nbn, nbt = (N + 127) // 128, (M + 127) // 128
+    tiles = nbn * nbt
+    total = tiles * G
+    P = min(2 * cus, max(1, total // 4))
+    if P > 8:
+        P &= ~7
+    part = mem.alloc(2 * P * 128 * 128 * 8)
+    cnt = mem.alloc(max(tiles, 1 << 12) * 4)
+    x_d, sx_d, mx_d = acts(mem, xq, sx, mx)
+    pf = wq + sizes(N, K, bits)[2] // 2
+    p = E.Program(asm['prefill.hip'], f'k_prefillILi{bits}E')
+    E.launch(p, mem, P, 256, p.pack_args([pf, c, m, N, K, x_d, sx_d, mx_d, M, out, nbt, tiles, P, part, cnt]))
+
+
+def test_prefill_parts_and_accumulate(asm):
+    """Three ragged parts (widths 37, 64, 35: unaligned boundaries take the per-column stores), then the same GEMM
+    accumulated onto a prefilled output."""
+    rng = oracle.Rng(12)
+    bits, N, K, M = 6, 136, 640, 130
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    want = oracle.gemm(rows, N, K, bits, xq, sx, mx)
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    widths = (37, 64, 35)
+    offs = (0, 37, 101, 136, 0)
+    dsts = [mem.alloc(M * w_ * 4) for w_ in widths]
+    run_prefill_out(asm, mem, lin, N, K, bits, xq, sx, mx, M, 3,
+                    out_struct(0, nparts=3, offs=offs, dsts=dsts + [0]))
+    for i, w_ in enumerate(widths):
+        got = mem.array(dsts[i], np.float32, M * w_).reshape(M, w_)
+        d = same_f32(want[:, offs[i]:offs[i] + w_], got)
+        assert d is None, (i, d)
+    base = np.random.default_rng(3).standard_normal((M, N)).astype(np.float32)
+    y = mem.alloc(M * N * 4, base)
+    run_prefill_out(asm, mem, lin, N, K, bits, xq, sx, mx, M, 3, out_struct(y, acc=1))
+    d = same_f32((base + want).astype(np.float32), mem.array(y, np.float32, M * N).reshape(M, N))
+    assert d is None, d
+
+
+@pytest.mark.parametrize('bits,cus', [(8, 1), (4, 1), (6, 8)])
+def test_prefill2_widths_and_k_slices(asm, bits, cus):
+    """k_prefill2 at W8 and W4, and at W6 with K-slices (one tile, 32 groups, cus = 8: two slices combined by the
+    last to arrive)."""
+    rng = oracle.Rng(30 + bits)
+    N, K, M = (72, 384, 70) if cus == 1 else (64, 4096, 70)
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    got, KS = run_prefill2(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus=cus)
+    assert KS == (1 if cus == 1 else 2)
+    d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+    assert d is None, d

@@ -106,8 +106,8 @@ SOURCES = sorted(f for f in os.listdir(w.CSRC) if f.endswith('.hip'))
 
 @needs_hipcc
 @pytest.mark.parametrize('source', SOURCES)
-def test_kernels_wait_for_their_loads(source, tmp_path):
-    asm = w.compile_asm(os.path.join(w.CSRC, source), str(tmp_path / 'k.s'))
+def test_kernels_wait_for_their_loads(source):
+    asm = w.asm_of(os.path.join(w.CSRC, source))
     ks = w.kernels(asm)
     if source == 'prefill.hip':
         assert sum('k_prefillILi' in n for n in ks) == 3, sorted(ks)
@@ -117,10 +117,10 @@ def test_kernels_wait_for_their_loads(source, tmp_path):
 
 @needs_hipcc
 @pytest.mark.parametrize('bits', [4, 6])
-def test_prefill_group_loop_keeps_its_prefetch(bits, tmp_path):
+def test_prefill_group_loop_keeps_its_prefetch(bits):
     """The group loop of k_prefill<4|6> holds no spill reload and no full drain: either would make the compiler wait
     for every copy in flight (vmcnt(0)), including the activation copies two groups ahead."""
-    asm = w.compile_asm(os.path.join(w.CSRC, 'prefill.hip'), str(tmp_path / 'k.s'))
+    asm = w.asm_of(os.path.join(w.CSRC, 'prefill.hip'))
     name = [n for n in w.kernels(asm) if f'k_prefillILi{bits}E' in n][0]
     items = w.parse(w.kernels(asm)[name])
     labels = {it[1]: i for i, it in enumerate(items) if it[0] == 'label'}
