@@ -47,6 +47,9 @@ class EmuError(Exception):
     pass
 
 
+_LANE_MASKS = {}            # EXEC value -> per-lane bools (read-only, shared)
+
+
 # ------------------------------------------------------------------------------------------------ device memory
 class Memory:
     """A flat device address space of numpy byte buffers."""
@@ -79,6 +82,38 @@ class Memory:
         data = np.asarray(data, np.uint8)
         arr, off = self.find(addr, data.size)
         arr[off:off + data.size] = data
+
+    def gather(self, addr, size, mask):
+        """(64, size) bytes at addr[l] .. + size for the lanes in mask (others 0)."""
+        out = np.zeros((64, size), np.uint8)
+        lanes = np.nonzero(mask)[0]
+        if lanes.size == 0:
+            return out
+        a = addr[lanes].astype(np.int64)
+        lo, hi = int(a.min()), int(a.max()) + size
+        try:
+            arr, off = self.find(lo, hi - lo)
+        except EmuError:                       # lanes in different buffers (Parts outputs): one at a time
+            for l in lanes:
+                out[l] = self.read(int(addr[l]), size)
+            return out
+        out[lanes] = arr[(a - lo + off)[:, None] + np.arange(size)]
+        return out
+
+    def scatter(self, addr, data, mask):
+        lanes = np.nonzero(mask)[0]
+        if lanes.size == 0:
+            return
+        size = data.shape[1]
+        a = addr[lanes].astype(np.int64)
+        lo, hi = int(a.min()), int(a.max()) + size
+        try:
+            arr, off = self.find(lo, hi - lo)
+        except EmuError:
+            for l in lanes:
+                self.write(int(addr[l]), data[l])
+            return
+        arr[(a - lo + off)[:, None] + np.arange(size)] = data[lanes]
 
     def array(self, base, dtype, count):
         arr, off = self.find(base, np.dtype(dtype).itemsize * count)
@@ -200,7 +235,7 @@ class Program:
         s[0:1] and the workgroup id in s2 as for the library's kernels."""
         p = cls.__new__(cls)
         p.name, p.lds_bytes, p.private_bytes = 'snippet', lds_bytes, private_bytes
-        p.user_sgprs, p.kernarg_size, p.args, p.hidden = 2, 8, [], []
+        p.user_sgprs, p.kernarg_size, p.args, p.hidden, p.wg_id_y = 2, 8, [], [], 0
         p.instrs, labels = [], {}
         for line in lines:
             s = line.split(';')[0].strip()
@@ -246,9 +281,10 @@ class Program:
         self.lds_bytes = int(d['amdhsa_group_segment_fixed_size'])
         self.private_bytes = int(d['amdhsa_private_segment_fixed_size'])
         self.user_sgprs = int(d['amdhsa_user_sgpr_count'])
+        self.wg_id_y = int(d.get('amdhsa_system_sgpr_workgroup_id_y', 0))
         for k in ('amdhsa_user_sgpr_dispatch_ptr', 'amdhsa_user_sgpr_queue_ptr', 'amdhsa_user_sgpr_dispatch_id',
-                  'amdhsa_user_sgpr_kernarg_preload_length', 'amdhsa_system_sgpr_workgroup_id_y',
-                  'amdhsa_system_sgpr_workgroup_id_z', 'amdhsa_system_sgpr_workgroup_info'):
+                  'amdhsa_user_sgpr_kernarg_preload_length', 'amdhsa_system_sgpr_workgroup_id_z',
+                  'amdhsa_system_sgpr_workgroup_info'):
             if int(d.get(k, 0)):
                 raise EmuError(f'{k} is not modelled')
         if not int(d['amdhsa_user_sgpr_kernarg_segment_ptr']) or self.user_sgprs != 2:
@@ -334,7 +370,13 @@ class Wave:
 
     def lanes(self):
         e = self.exec
-        return ((e >> LANES.astype(np.uint64)) & 1).astype(bool) if e != MASK64 else np.ones(64, bool)
+        m = _LANE_MASKS.get(e)
+        if m is None:
+            m = ((np.uint64(e) >> LANES.astype(np.uint64)) & np.uint64(1)).astype(bool)
+            m.flags.writeable = False
+            if len(_LANE_MASKS) < 4096:
+                _LANE_MASKS[e] = m
+        return m
 
     # --- vector access
     def check_v(self, base, n, what):
@@ -344,15 +386,25 @@ class Wave:
                                f'while a load into it is pending')
 
     def vget(self, op, width=1):
-        """(64,) uint32 for width 1, (64,) uint64 for width 2."""
+        """(64,) uint32 for width 1, (64,) uint64 for width 2; abs / neg source modifiers act on the sign bit, as
+        for the float operands they are defined on (VOP3 bit moves such as v_cndmask take them too)."""
         if op.kind == 'v':
             self.check_v(op.base, width, 'reads')
             if width == 1:
-                return self.v[op.base].copy()
-            return self.v[op.base].astype(np.uint64) | (self.v[op.base + 1].astype(np.uint64) << np.uint64(32))
-        val = self.sget(op, width) if op.kind != 'lit' else (
-            op.value & MASK32 if width == 1 else op.value & MASK64)
-        return np.full(64, val, np.uint32 if width == 1 else np.uint64)
+                x = self.v[op.base].copy()
+            else:
+                x = self.v[op.base].astype(np.uint64) | (self.v[op.base + 1].astype(np.uint64) << np.uint64(32))
+        else:
+            val = self.sget(op, width) if op.kind != 'lit' else (
+                op.value & MASK32 if width == 1 else op.value & MASK64)
+            x = np.full(64, val, np.uint32 if width == 1 else np.uint64)
+        if op.abs or op.neg:
+            sign = np.uint32(0x80000000) if width == 1 else np.uint64(1 << 63)
+            if op.abs:
+                x = x & ~sign
+            if op.neg:
+                x = x ^ sign
+        return x
 
     def vset(self, op, val, width=1, mask=None):
         if op.kind != 'v':
@@ -382,7 +434,7 @@ class Wave:
             bits = v & MASK64 if -16 <= v <= 64 else (v & MASK32) << 32
             x = np.full(64, bits, np.uint64).view(np.float64)
         else:
-            x = self.vget(op, 1 if dtype == np.float32 else 2).view(dtype)
+            return self.vget(op, 1 if dtype == np.float32 else 2).view(dtype)      # modifiers applied there
         if op.abs:
             x = np.abs(x)
         if op.neg:
@@ -410,15 +462,51 @@ def bits_of(v):
 
 
 def exact_fma(a, b, c, dtype):
+    """a * b + c rounded once (round to nearest even)."""
+    a, b, c = np.asarray(a, dtype), np.asarray(b, dtype), np.asarray(c, dtype)
     out = np.empty(64, dtype)
-    for i in range(64):
-        x, y, z = float(a[i]), float(b[i]), float(c[i])
+    with np.errstate(all='ignore'):
+        if dtype == np.float32:
+            # the product of two binary32 values is exact in binary64; s = RN64(p + c) with its exact error e (TwoSum).
+            # RN32 of the exact sum differs from RN32(s) only when s is a binary32 midpoint and e != 0
+            p = a.astype(np.float64) * b.astype(np.float64)
+            c64 = c.astype(np.float64)
+            s = p + c64
+            bb = s - p
+            e = (p - (s - bb)) + (c64 - bb)
+            r = s.astype(np.float32)
+            up, dn = np.nextafter(r, np.float32(np.inf)), np.nextafter(r, np.float32(-np.inf))
+            fix = np.isfinite(s) & (e != 0)
+            mid_up = fix & (s == (r.astype(np.float64) + up.astype(np.float64)) / 2)
+            mid_dn = fix & (s == (r.astype(np.float64) + dn.astype(np.float64)) / 2)
+            r = np.where(mid_up & (e > 0), up, r)
+            r = np.where(mid_dn & (e < 0), dn, r)
+            out[:] = r
+            return out
+        # binary64: exact when the product is (then one rounding of p + c); otherwise exact rational arithmetic
+        p = a * b
+        exact = np.isfinite(p) & (p == 0) | _product_exact(a, b, p)
+        out[:] = p + c
+    for k in np.nonzero(~exact)[0]:
+        x, y, z = float(a[k]), float(b[k]), float(c[k])
         if not (np.isfinite(x) and np.isfinite(y) and np.isfinite(z)):
-            out[i] = dtype(x * y + z) if dtype == np.float64 else np.float32(np.float64(x) * np.float64(y) + np.float64(z))
+            out[k] = x * y + z
             continue
-        f = Fraction(x) * Fraction(y) + Fraction(z)
-        out[i] = round_fraction(f, dtype)
+        out[k] = round_fraction(Fraction(x) * Fraction(y) + Fraction(z), dtype)
     return out
+
+
+def _product_exact(a, b, p):
+    """a * b == p exactly, by Dekker's splitting (error-free product in binary64)."""
+    with np.errstate(all='ignore'):
+        def split(x):
+            t = x * 134217729.0
+            hi = t - (t - x)
+            return hi, x - hi
+        ah, al = split(a)
+        bh, bl = split(b)
+        err = ((ah * bh - p) + ah * bl + al * bh) + al * bl
+        return np.isfinite(p) & (err == 0) & (np.abs(a) < 1e300) & (np.abs(b) < 1e300)
 
 
 def round_fraction(f, dtype):
@@ -667,6 +755,13 @@ def _(w, i):
 def _(w, i): w.scc = (w.sget(i.ops[0]) >> (w.sget(i.ops[1]) & 31)) & 1
 
 
+@op('s_not_b32')
+def _(w, i):
+    r = ~w.sget(i.ops[1]) & MASK32
+    w.sset(i.ops[0], r)
+    w.scc = int(r != 0)
+
+
 @op('s_bitset1_b32')
 def _(w, i): w.sset(i.ops[0], w.sget(i.ops[0]) | (1 << (w.sget(i.ops[1]) & 31)))
 
@@ -810,6 +905,7 @@ H['v_mul_u32_u24'] = _v2(lambda a, b: (a & M24) * (b & M24))
 H['v_mul_lo_u32'] = _v2(lambda a, b: (a * b))
 H['v_mul_hi_u32'] = _v2(lambda a, b: (a * b) >> np.uint64(32))
 H['v_min_u32'] = _v2(lambda a, b: np.minimum(a, b))
+H['v_max_u32'] = _v2(lambda a, b: np.maximum(a, b))
 H['v_add3_u32'] = _v3(lambda a, b, c: a + b + c)
 H['v_or3_b32'] = _v3(lambda a, b, c: a | b | c)
 H['v_xad_u32'] = _v3(lambda a, b, c: (a ^ b) + c)
@@ -1015,8 +1111,24 @@ def _vcmp(w, i):
 
 
 for _c in ('eq', 'ne', 'lt', 'le', 'gt', 'ge', 'lg'):
-    for _t in ('i32', 'u32', 'i64', 'u64', 'f32'):
+    for _t in ('i32', 'u32', 'i64', 'u64', 'f32', 'f64'):
         H[f'v_cmp_{_c}_{_t}'] = _vcmp
+
+# float compares: o / u (ordered / unordered) and the negated forms, true when either operand is NaN
+FCMP = {'o': lambda a, b: ~(np.isnan(a) | np.isnan(b)), 'u': lambda a, b: np.isnan(a) | np.isnan(b),
+        'nge': lambda a, b: ~(a >= b), 'nlg': lambda a, b: ~((a < b) | (a > b)), 'ngt': lambda a, b: ~(a > b),
+        'nle': lambda a, b: ~(a <= b), 'neq': lambda a, b: ~(a == b), 'nlt': lambda a, b: ~(a < b)}
+
+
+def _vfcmp(w, i):
+    m = re.match(r'v_cmp_(\w+?)_f(32|64)$', i.mn)
+    dt = np.float32 if m.group(2) == '32' else np.float64
+    with np.errstate(invalid='ignore'):
+        set_mask(w, i.ops[0], FCMP[m.group(1)](w.fsrc(i.ops[1], dt), w.fsrc(i.ops[2], dt)))
+
+
+for _c in FCMP:
+    H[f'v_cmp_{_c}_f32'] = H[f'v_cmp_{_c}_f64'] = _vfcmp
 
 
 # --- 64-bit integer
@@ -1024,16 +1136,14 @@ for _c in ('eq', 'ne', 'lt', 'le', 'gt', 'ge', 'lg'):
 def _(w, i):
     a, b = w.vget(i.ops[2]), w.vget(i.ops[3])
     c = w.vget(i.ops[4], 2)
-    act = w.lanes()
-    res = np.zeros(64, np.uint64)
-    carry = np.zeros(64, bool)
-    for l in np.nonzero(act)[0]:
-        if i.mn == 'v_mad_u64_u32':
-            r = int(a[l]) * int(b[l]) + int(c[l])
-        else:
-            r = sx32(int(a[l])) * sx32(int(b[l])) + (int(c[l]) - (1 << 64) if int(c[l]) >> 63 else int(c[l]))
-        res[l] = r & MASK64
-        carry[l] = (r >> 64) != 0 if i.mn == 'v_mad_u64_u32' else False
+    if i.mn == 'v_mad_u64_u32':
+        prod = a.astype(np.uint64) * b.astype(np.uint64)           # exact: below 2^64
+        res = prod + c                                             # modulo 2^64
+        carry = res < prod
+    else:
+        prod = (i32(a).astype(np.int64) * i32(b).astype(np.int64)).view(np.uint64)
+        res = prod + c
+        carry = np.zeros(64, bool)
     w.vset(i.ops[0], res, 2)
     if i.ops[1].kind == 's':
         set_mask(w, i.ops[1], carry)
@@ -1107,6 +1217,19 @@ def _(w, i):
         w.vset(i.ops[0], (np.float32(1.0) / w.fsrc(i.ops[1])).astype(np.float32).view(np.uint32))
 
 
+@op('v_floor_f32')
+def _(w, i): w.vset(i.ops[0], np.floor(w.fsrc(i.ops[1])).astype(np.float32).view(np.uint32))
+
+
+@op('v_mad_i32_i24')
+def _(w, i):
+    def s24(x):
+        x = (x & 0xFFFFFF).astype(np.int64)
+        return np.where(x & 0x800000, x - 0x1000000, x)
+    a, b = s24(w.vget(i.ops[1]).astype(np.int64)), s24(w.vget(i.ops[2]).astype(np.int64))
+    w.vset(i.ops[0], ((a * b + i32(w.vget(i.ops[3])).astype(np.int64)) & MASK32).astype(np.uint32))
+
+
 @op('v_trunc_f32')
 def _(w, i): w.vset(i.ops[0], np.trunc(w.fsrc(i.ops[1])).astype(np.float32).view(np.uint32))
 
@@ -1159,29 +1282,42 @@ def _(w, i): w.vset(i.ops[0], w.fsrc(i.ops[1], np.float64).astype(np.float32).vi
 
 
 # --- matrix core
+# layout maps of v_mfma_i32_32x32x32_i8: operand element (row or column r, k) is lane r + 32 (k // 16), byte k % 16;
+# result element (i, j) is lane j + 32 ((i // 4) % 2), register 4 (i // 8) + i % 4
+_MF_R, _MF_K = np.meshgrid(np.arange(32), np.arange(32), indexing='ij')
+_MF_LANE, _MF_BYTE = _MF_R + 32 * (_MF_K // 16), _MF_K % 16
+_MF_I, _MF_J = np.meshgrid(np.arange(32), np.arange(32), indexing='ij')
+_MF_DLANE, _MF_DREG = _MF_J + 32 * ((_MF_I // 4) % 2), 4 * (_MF_I // 8) + _MF_I % 4
+
+
 @op('v_mfma_i32_32x32x32_i8')
 def _(w, i):
     d, a, b, c = i.ops
-    A = np.stack([w.vget(Op(f'v{a.base + k}')) for k in range(4)], 1).view(np.int8).reshape(64, 16)
-    B = np.stack([w.vget(Op(f'v{b.base + k}')) for k in range(4)], 1).view(np.int8).reshape(64, 16)
-    Am = np.zeros((32, 32), np.int64)
-    Bm = np.zeros((32, 32), np.int64)
-    for l in range(64):
-        Am[l % 32, 16 * (l // 32):16 * (l // 32) + 16] = A[l]
-        Bm[16 * (l // 32):16 * (l // 32) + 16, l % 32] = B[l]
+    w.check_v(a.base, 4, 'reads')
+    w.check_v(b.base, 4, 'reads')
+    A = w.v[a.base:a.base + 4].T.copy().view(np.int8).reshape(64, 16)
+    B = w.v[b.base:b.base + 4].T.copy().view(np.int8).reshape(64, 16)
+    Am = A[_MF_LANE, _MF_BYTE].astype(np.int64)                 # [row][k]
+    Bm = B[_MF_LANE, _MF_BYTE].astype(np.int64).T               # [k][col]
     if c.kind == 'lit':
         Cm = np.full((32, 32), c.value, np.int64)
     else:
-        Creg = np.stack([w.vget(Op(f'v{c.base + k}')) for k in range(16)], 1).view(np.int32)
-        Cm = np.zeros((32, 32), np.int64)
-        for ii in range(32):
-            Cm[ii, :] = Creg[np.arange(32) + 32 * ((ii // 4) % 2), 4 * (ii // 8) + ii % 4]
-    D = (Am @ Bm + Cm) & MASK32
+        w.check_v(c.base, 16, 'reads')
+        Creg = w.v[c.base:c.base + 16].T.view(np.int32)
+        Cm = Creg[_MF_DLANE, _MF_DREG].astype(np.int64)
+    D = ((Am @ Bm + Cm) & MASK32).astype(np.uint32)
     out = np.zeros((64, 16), np.uint32)
-    for ii in range(32):
-        out[np.arange(32) + 32 * ((ii // 4) % 2), 4 * (ii // 8) + ii % 4] = D[ii, :].astype(np.uint32)
+    out[_MF_DLANE, _MF_DREG] = D
     w.check_v(d.base, 16, 'writes')
-    w.vset_regs(d.base, out, np.ones(64, bool))
+    w.v[d.base:d.base + 16] = out.T
+
+
+@op('v_dot4c_i32_i8')
+def _(w, i):
+    a = w.vget(i.ops[1]).view(np.int8).reshape(64, 4).astype(np.int64)
+    b = w.vget(i.ops[2]).view(np.int8).reshape(64, 4).astype(np.int64)
+    d = i32(w.vget(i.ops[0])).astype(np.int64)
+    w.vset(i.ops[0], ((d + (a * b).sum(1)) & MASK32).astype(np.uint32))
 
 
 # --- LDS
@@ -1209,6 +1345,40 @@ def _(w, i):
         return
     w.check_v(i.ops[0].base, size // 4, 'writes')
     w.vset_regs(i.ops[0].base, data.view(np.uint32).reshape(64, size // 4), act)
+
+
+@op('ds_read2st64_b64', 'ds_read2_b64')
+def _(w, i):
+    act = w.lanes()
+    addr = _ds_addr(w, i.ops[1])
+    unit = 512 if 'st64' in i.mn else 8
+    out = np.zeros((64, 4), np.uint32)
+    for k, key in enumerate(('offset0', 'offset1')):
+        out[:, 2 * k:2 * k + 2] = w.wg.lds_read(addr + int(i.mods.get(key, 0)) * unit, 8, act, w).view(np.uint32)
+    w.check_v(i.ops[0].base, 4, 'writes')
+    w.vset_regs(i.ops[0].base, out, act)
+
+
+@op('ds_write2st64_b64', 'ds_write2_b64')
+def _(w, i):
+    act = w.lanes()
+    addr = _ds_addr(w, i.ops[0])
+    unit = 512 if 'st64' in i.mn else 8
+    for k, key in enumerate(('offset0', 'offset1')):
+        data = w.vget(i.ops[1 + k], 2).view(np.uint8).reshape(64, 8)
+        w.wg.lds_write(addr + int(i.mods.get(key, 0)) * unit, data, act, w)
+
+
+@op('ds_add_u64')
+def _(w, i):
+    act = w.lanes()
+    addr = _ds_addr(w, i.ops[0]) + int(i.mods.get('offset', 0))
+    val = w.vget(i.ops[1], 2)
+    for l in np.nonzero(act)[0]:               # lanes in order: the adds commute
+        a = int(addr[l])
+        old_ = w.wg.lds_read(np.full(64, a), 8, np.eye(64, dtype=bool)[0], w)[0].view(np.uint64)[0]
+        new_ = np.array([(int(old_) + int(val[l])) & MASK64], np.uint64).view(np.uint8)
+        w.wg.lds_write(np.full(64, a), np.tile(new_, (64, 1)), np.eye(64, dtype=bool)[0], w)
 
 
 @op('ds_write_b8', 'ds_write_b16', 'ds_write_b32', 'ds_write_b64', 'ds_write_b128')
@@ -1256,13 +1426,15 @@ def _(w, i):
     voff = w.vget(vaddr_op).astype(np.int64) if 'offen' in i.mods else np.zeros(64, np.int64)
     ioff = parse_int(str(i.mods.get('offset', 0)))
     soff = w.sget(so_op) if so_op.kind in ('s', 'lit') else 0
+    # range check per dword (per element below a dword): in range when per-lane offset + instruction offset + the
+    # element's offset < num_records; the scalar offset is added after the check
+    off = voff + ioff
+    step = 4 if size >= 4 else size
     data = np.zeros((64, size), np.uint8)
-    for l in np.nonzero(act)[0]:
-        off = int(voff[l]) + ioff
-        for k in range(0, size, 4 if size >= 4 else size):
-            n = min(4, size - k)
-            if off + k < nrec:
-                data[l, k:k + n] = w.wg.mem.read(base + soff + off + k, n)
+    for k in range(0, size, step):
+        ok = act & (off + k < nrec)
+        if ok.any():
+            data[:, k:k + step] = w.wg.mem.gather(base + soff + off + k, step, ok)
     if to_lds:
         m0 = w.s[124] & 0x3FFFF
         dst = m0 + ioff + size * LANES
@@ -1303,8 +1475,7 @@ def _(w, i):
             'global_load_ubyte': 1, 'global_load_sbyte': 1, 'global_load_sshort': 2}[i.mn]
     addr, act = _gaddr(w, i, i.ops[1], i.ops[2])
     data = np.zeros((64, max(size, 4)), np.uint8)
-    for l in np.nonzero(act)[0]:
-        data[l, :size] = w.wg.mem.read(int(addr[l]), size)
+    data[:, :size] = w.wg.mem.gather(addr, size, act)
     if i.mn in ('global_load_sbyte', 'global_load_sshort'):       # sign-extended into the dword
         neg = (data[:, size - 1] & 0x80) != 0
         data[neg, size:] = 0xFF
@@ -1318,9 +1489,9 @@ def _(w, i):
             'global_store_byte': 1}[i.mn]
     addr, act = _gaddr(w, i, i.ops[0], i.ops[2])
     nreg = max(1, size // 4)
-    data = np.stack([w.vget(Op(f'v{i.ops[1].base + k}')) for k in range(nreg)], 1).view(np.uint8)
-    for l in np.nonzero(act)[0]:
-        w.wg.mem.write(int(addr[l]), data[l, :size])
+    w.check_v(i.ops[1].base, nreg, 'reads')
+    data = w.v[i.ops[1].base:i.ops[1].base + nreg].T.copy().view(np.uint8)
+    w.wg.mem.scatter(addr, data[:, :size], act)
     w.queue.append(Pending())
 
 
@@ -1341,6 +1512,28 @@ def _(w, i):
         w.wg.mem.write(a, np.array([(o + int(val[l])) & MASK32], np.uint32).view(np.uint8))
     if ret:
         issue_load(w, vdst.base, old.reshape(64, 1), act)
+    else:
+        w.queue.append(Pending())
+
+
+@op('global_atomic_add_x2', 'global_atomic_swap_x2')
+def _(w, i):
+    ret = 'sc0' in i.mods or 'glc' in i.mods
+    if ret:
+        vdst, vaddr, vdata, saddr = i.ops
+    else:
+        vaddr, vdata, saddr = i.ops
+    addr, act = _gaddr(w, i, vaddr, saddr)
+    val = w.vget(vdata, 2)
+    old = np.zeros((64, 2), np.uint32)
+    for l in np.nonzero(act)[0]:
+        a = int(addr[l])
+        o = int(w.wg.mem.read(a, 8).view(np.uint64)[0])
+        old[l] = np.array([o], np.uint64).view(np.uint32)
+        n = (o + int(val[l])) & MASK64 if i.mn == 'global_atomic_add_x2' else int(val[l])
+        w.wg.mem.write(a, np.array([n], np.uint64).view(np.uint8))
+    if ret:
+        issue_load(w, vdst.base, old, act)
     else:
         w.queue.append(Pending())
 
@@ -1380,15 +1573,18 @@ def _scratch_off(w, i, vaddr, saddr):
 
 # ------------------------------------------------------------------------------------------------ workgroups
 class Workgroup:
-    def __init__(self, prog, mem, wg_id, nthreads):
+    def __init__(self, prog, mem, wg_id, nthreads, wg_id_y=0, dyn_lds=0):
         self.prog, self.mem = prog, mem
-        self.lds = np.zeros(max(prog.lds_bytes, 4) + 16, np.uint8)
+        self.lds_size = prog.lds_bytes + dyn_lds
+        self.lds = np.zeros(max(self.lds_size, 4) + 16, np.uint8)
         self.lds_busy = np.zeros(self.lds.size, np.int32)     # bytes that pending copies will write
         self.waves = []
         for wv in range((nthreads + 63) // 64):
             w = Wave(self, wv, prog)
             w.s[0], w.s[1] = KERNARG & MASK32, KERNARG >> 32
             w.s[2] = wg_id
+            if prog.wg_id_y:
+                w.s[3] = wg_id_y
             tid = wv * 64 + LANES
             w.v[0] = tid.astype(np.uint32)
             n = min(64, nthreads - wv * 64)
@@ -1396,39 +1592,41 @@ class Workgroup:
             self.waves.append(w)
 
     def lds_check(self, addr, size, act, w, what):
-        for l in np.nonzero(act)[0]:
-            a = int(addr[l])
-            if a < 0 or a + size > self.lds.size:
-                raise EmuError(f'LDS {what} of {size} bytes at {a} outside the {self.prog.lds_bytes} allocated')
-            if self.lds_busy[a:a + size].any():
-                raise EmuError(f'wave {w.wid} pc {w.pc} ({self.prog.instrs[w.pc].text}): LDS {what} at {a} while a '
-                               f'copy into it is pending')
+        a = addr[act].astype(np.int64)
+        if a.size == 0:
+            return None
+        if a.min() < 0 or a.max() + size > self.lds_size:
+            raise EmuError(f'LDS {what} of {size} bytes at {int(a.min())}..{int(a.max())} outside the {self.lds_size} '
+                           f'allocated')
+        idx = a[:, None] + np.arange(size)
+        if self.lds_busy[idx].any():
+            raise EmuError(f'wave {w.wid} pc {w.pc} ({self.prog.instrs[w.pc].text}): LDS {what} at {int(a.min())} '
+                           f'while a copy into it is pending')
+        return idx
 
     def lds_read(self, addr, size, act, w):
-        self.lds_check(addr, size, act, w, 'read')
+        idx = self.lds_check(addr, size, act, w, 'read')
         out = np.zeros((64, size), np.uint8)
-        for l in np.nonzero(act)[0]:
-            out[l] = self.lds[int(addr[l]):int(addr[l]) + size]
+        if idx is not None:
+            out[act] = self.lds[idx]
         return out
 
     def lds_write(self, addr, data, act, w):
-        size = data.shape[1]
-        self.lds_check(addr, size, act, w, 'write')
-        for l in np.nonzero(act)[0]:
-            self.lds[int(addr[l]):int(addr[l]) + size] = data[l]
+        idx = self.lds_check(addr, data.shape[1], act, w, 'write')
+        if idx is not None:
+            self.lds[idx] = data[act]
 
     def lds_pending(self, w, dst, size, act, data):
-        self.lds_check(dst, size, act, w, 'copy')
-        for l in np.nonzero(act)[0]:
-            self.lds_busy[int(dst[l]):int(dst[l]) + size] += 1
+        idx = self.lds_check(dst, size, act, w, 'copy')
+        if idx is not None:
+            np.add.at(self.lds_busy, idx.ravel(), 1)
 
     def retire(self, w, p):
         if p.lds is not None:
             dst, size, act, data = p.lds
-            for l in np.nonzero(act)[0]:
-                a = int(dst[l])
-                self.lds_busy[a:a + size] -= 1
-                self.lds[a:a + size] = data[l]
+            idx = dst[act].astype(np.int64)[:, None] + np.arange(size)
+            np.subtract.at(self.lds_busy, idx.ravel(), 1)
+            self.lds[idx] = data[act]
         elif p.regs is not None:
             for k, r in enumerate(p.regs):
                 w.pending_v[r] -= 1
@@ -1478,18 +1676,26 @@ HIDDEN = {'hidden_block_count_x': lambda g, b: g, 'hidden_block_count_y': lambda
           'hidden_remainder_z': lambda g, b: 0, 'hidden_grid_dims': lambda g, b: 1}
 
 
-def launch(prog, mem, grid, block, kernarg_bytes):
-    """Runs every workgroup of a 1-D grid in order."""
+def launch(prog, mem, grid, block, kernarg_bytes, dyn_lds=0):
+    """Runs every workgroup of the grid (an int, or (x, y) for a 2-D grid) in order, x fastest."""
     if len(kernarg_bytes) > prog.kernarg_size:
         raise EmuError('kernel arguments larger than the kernel expects')
     ka = np.zeros(max(prog.kernarg_size, 8) + 64, np.uint8)
     ka[:len(kernarg_bytes)] = np.frombuffer(bytes(kernarg_bytes), np.uint8)
+    gx, gy = (grid, 1) if isinstance(grid, int) else grid
+    if gy > 1 and not prog.wg_id_y:
+        raise EmuError('a 2-D grid for a kernel that does not read its y workgroup id')
     for off, size, kind in prog.hidden:        # launch dimensions; every other hidden argument (queues, heaps) is 0
-        v = HIDDEN[kind](grid, block) if kind in HIDDEN else 0
+        v = HIDDEN[kind](gx, block) if kind in HIDDEN else 0
+        if kind == 'hidden_block_count_y':
+            v = gy
+        if kind == 'hidden_dynamic_lds_size':
+            v = dyn_lds
         ka[off:off + size] = np.frombuffer(int(v).to_bytes(size, 'little'), np.uint8)
     mem.bufs = [b for b in mem.bufs if b[0] != KERNARG]
     mem.bufs.append((KERNARG, ka))
     steps = 0
-    for g in range(grid):
-        steps += Workgroup(prog, mem, g, block).run()
+    for y in range(gy):
+        for x in range(gx):
+            steps += Workgroup(prog, mem, x, block, y, dyn_lds).run()
     return steps

@@ -124,3 +124,30 @@ def test_mfma_identity():
     D = w.v[32:48].T.view(np.int32)
     for i in range(32):
         assert (D[np.arange(32) + 32 * ((i // 4) % 2), 4 * (i // 8) + i % 4] == Bm[i] + Cm[i]).all()
+
+
+def test_fma_rounds_once():
+    """The emulator's fused multiply-add against exact rational arithmetic: random operands over wide exponent ranges,
+    and products that are exactly a binary32 midpoint (p = (2^12 + 1)(2^12 + 3) = 2^24 + 2^14 + 3, odd, between two
+    binary32 neighbours 2 apart) with a tiny addend of either sign, where a binary64 sum alone would round to the
+    midpoint and then to even."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    for trial in range(40):
+        a = (rng.standard_normal(64) * 2.0 ** rng.integers(-30, 30, 64)).astype(np.float32)
+        b = (rng.standard_normal(64) * 2.0 ** rng.integers(-30, 30, 64)).astype(np.float32)
+        c = (rng.standard_normal(64) * 2.0 ** rng.integers(-60, 60, 64)).astype(np.float32)
+        if trial == 0:
+            a[:8], b[:8] = np.float32(4097.0), np.float32(4099.0)
+            c[:8] = np.float32(2.0 ** -30) * np.array([1, -1, 1, -1, 3, -3, 0.5, -0.5], np.float32)
+        got = E.exact_fma(a, b, c, np.float32)
+        want = np.array([E.round_fraction(Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z)), np.float32)
+                         for x, y, z in zip(a, b, c)], np.float32)
+        assert (got.view(np.uint32) == want.view(np.uint32)).all(), trial
+    # 4097 * 4101 = 2^24 + 24581: a midpoint whose even neighbour is the lower one; a tiny positive addend rounds up
+    got = E.exact_fma(np.full(64, 4097.0, np.float32), np.full(64, 4101.0, np.float32),
+                      np.full(64, 2.0 ** -30, np.float32), np.float32)
+    assert got[0] == np.float32(2 ** 24 + 24582)
+    got = E.exact_fma(np.full(64, 4097.0, np.float32), np.full(64, 4101.0, np.float32),
+                      np.zeros(64, np.float32), np.float32)
+    assert got[0] == np.float32(2 ** 24 + 24580)                 # the tie itself goes to even: down

@@ -260,3 +260,88 @@ def test_prefill2_widths_and_k_slices(asm, bits, cus):
     assert KS == (1 if cus == 1 else 2)
     d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
     assert d is None, d
+
+
+# ------------------------------------------------------------------ decode kernels (launch_decode, launch_decode_ms)
+def run_decode(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus):
+    wq, c, m = lin
+    MP = 1 if M <= 1 else 4 if M <= 4 else 8 if M <= 8 else 16
+    G, T = K // GROUP, (N + 63) // 64
+    waves = 8 * cus
+    KS = 1
+    if 2 * T < cus:
+        KS = max(1, min((cus + T - 1) // T, (G + 3) // 4))
+    gs = (G + KS - 1) // KS
+    S = (waves + T * KS - 1) // (T * KS)
+    S = max(1, min(S, min(gs, min(8 if MP >= 4 else 16, 128 // MP))))
+    part = mem.alloc(MP * T * 64 * 8) if KS > 1 else 0
+    cnt = mem.alloc(T * 4) if KS > 1 else 0
+    y = mem.alloc(M * N * 4)
+    x_d, sx_d, mx_d = acts(mem, xq, sx, mx)
+    p = E.Program(asm['gemm.hip'], f'k_decodeILi{bits}ELi{MP}ELb0E')
+    E.launch(p, mem, T * KS, 64 * S,
+             p.pack_args([wq, c, m, N, K, x_d, sx_d, mx_d, M, out_struct(y), KS, part, cnt]),
+             dyn_lds=S * MP * 64 * 8 if S > 1 else 0)
+    if KS > 1:
+        assert (mem.array(part, np.int64, MP * T * 64) == 0).all() and (mem.array(cnt, np.uint32, T) == 0).all(), \
+            'K-split buffers not left at zero'
+    return mem.array(y, np.float32, M * N).reshape(M, N).copy(), MP, KS, S
+
+
+def dms_slices(units, G, cus):
+    KS = 1 if units >= cus else max(1, min((cus + units - 1) // units, G // 16))
+    KS = max(KS, (G + 95) // 96)
+    gs = (G + KS - 1) // KS
+    return (G + gs - 1) // gs
+
+
+def run_decode_ms(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus):
+    wq, c, m = lin
+    G, T = K // GROUP, (N + 63) // 64
+    split = M > 32 and 2 * T * dms_slices(2 * T, G, cus) > T * dms_slices(T, G, cus)
+    TS = 1 if (M <= 32 or split) else 2
+    MT = 32 * TS
+    NB = (M + MT - 1) // MT
+    units = T * NB
+    KS = dms_slices(units, G, cus)
+    gs = (G + KS - 1) // KS
+    P = min(4 if units * KS <= cus else 2, gs)
+    part = mem.alloc(NB * KS * MT * T * 64 * 8) if KS > 1 else 0
+    cnt = mem.alloc(max(units, 1 << 14) * 4) if KS > 1 else 0
+    NS = (gs + 31) & ~31
+    lds = max(2 * P * MT * 128, MT * 64 * 8) + 3 * (64 + MT) * NS
+    y = mem.alloc(M * N * 4)
+    x_d, sx_d, mx_d = acts(mem, xq, sx, mx)
+    p = E.Program(asm['gemm.hip'], f'k_decode_msILi{bits}ELi{TS}E')
+    E.launch(p, mem, (T * KS, NB), 128 * P,
+             p.pack_args([wq, c, m, N, K, x_d, sx_d, mx_d, M, out_struct(y), KS, part, cnt]), dyn_lds=lds)
+    return mem.array(y, np.float32, M * N).reshape(M, N).copy(), TS, KS, P
+
+
+@pytest.mark.parametrize('bits,M,cus', [(6, 1, 4), (6, 1, 16), (8, 4, 4), (4, 8, 16), (6, 16, 4)])
+def test_decode_matches_oracle(asm, bits, M, cus):
+    """k_decode (M <= 16) through every token count form, with and without the K-split (cus = 16: the tiles fill
+    less than half the CUs, so K-slices meet through int64 atomics and the last to arrive finishes)."""
+    rng = oracle.Rng(50 + bits + M)
+    N, K = 72, 1024
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    got, MP, KS, S = run_decode(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus)
+    assert (KS > 1) == (cus == 16)
+    d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+    assert d is None, (MP, KS, S, d)
+
+
+@pytest.mark.parametrize('bits,M,cus', [(6, 40, 4), (6, 64, 16), (8, 20, 4)])
+def test_decode_ms_matches_oracle(asm, bits, M, cus):
+    rng = oracle.Rng(60 + bits + M)
+    N, K = 72, 2048
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+    mem = E.Memory()
+    lin = repack(asm, mem, rows, N, K, bits)
+    got, TS, KS, P = run_decode_ms(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus)
+    d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+    assert d is None, (TS, KS, P, d)
