@@ -569,9 +569,72 @@ def _sdwa(w, i):
     w.vset(i.ops[0], field)
 
 
+def _dpp_src_lane(mods):
+    """The source lane of each lane for the DPP controls the library's kernels use (rows of 16 lanes)."""
+    l = LANES
+    if 'quad_perm' in mods:
+        perm = [int(x) for x in mods['quad_perm'].strip('[]').split(',')]
+        return (l & ~3) + np.array(perm)[l & 3]
+    if 'row_mirror' in mods:
+        return (l & ~15) + (15 - (l & 15))
+    if 'row_half_mirror' in mods:
+        return (l & ~7) + (7 - (l & 7))
+    raise EmuError(f'DPP control {mods} not modelled')
+
+
+def _dpp(w, i):
+    """src0 read from another lane of the row; a lane whose source lane is disabled reads 0 with bound_ctrl, else it
+    is not written."""
+    if i.mods.get('row_mask', '0xf') not in ('0xf', '15') or i.mods.get('bank_mask', '0xf') not in ('0xf', '15'):
+        raise EmuError('DPP row or bank masks not modelled')
+    src = _dpp_src_lane(i.mods)
+    act = w.lanes()
+    op0 = i.ops[1]
+    vals = w.vget(op0)[src]
+    src_on = act[src]
+    bound = str(i.mods.get('bound_ctrl', '0')) in ('1', 'True')
+    vals = np.where(src_on, vals, np.uint32(0))
+    write = act & (src_on | bound)
+    base = i.mn[:-4]
+    if base == 'v_mov_b32':
+        w.vset(i.ops[0], vals, mask=write)
+    elif base == 'v_add_f32':
+        with np.errstate(all='ignore'):
+            r = (vals.view(np.float32) + w.fsrc(i.ops[2])).astype(np.float32)
+        w.vset(i.ops[0], r.view(np.uint32), mask=write)
+    elif base == 'v_max_f32':
+        r = np.fmax(vals.view(np.float32), w.fsrc(i.ops[2])).astype(np.float32)
+        w.vset(i.ops[0], r.view(np.uint32), mask=write)
+    else:
+        raise EmuError(f'{i.mn} not modelled')
+
+
+@op('ds_bpermute_b32')
+def _(w, i):
+    act = w.lanes()
+    addr = w.vget(i.ops[1]).astype(np.int64) + int(i.mods.get('offset', 0))
+    data = w.vget(i.ops[2])
+    src = (addr // 4) % 64
+    tmp = np.where(act[src], data[src], np.uint32(0))
+    w.vset(i.ops[0], tmp, mask=act)
+
+
+def _cvt_sdwa(w, i):
+    if i.mods.get('src0_sel', 'DWORD') != 'DWORD' or i.mods.get('dst_unused', 'UNUSED_PAD') != 'UNUSED_PAD':
+        raise EmuError('sdwa conversion form not modelled')
+    x = w.fsrc(i.ops[1]).astype(np.float64)
+    r = np.where(np.isnan(x), 0, np.clip(np.trunc(x), -2 ** 31, 2 ** 31 - 1)).astype(np.int64) & MASK32
+    sh, nb = SEL[i.mods.get('dst_sel', 'DWORD')]
+    w.vset(i.ops[0], ((r & ((1 << nb) - 1)) << sh).astype(np.uint64))
+
+
 def handler(mn):
     if mn.endswith('_sdwa') and mn[:-5] in SDWA_OPS:
         return _sdwa
+    if mn == 'v_cvt_i32_f32_sdwa':
+        return _cvt_sdwa
+    if mn.endswith('_dpp') and mn[:-4] in ('v_mov_b32', 'v_add_f32', 'v_max_f32'):
+        return _dpp
     base = re.sub(r'_e(32|64)$', '', mn)
     if base in H:
         return H[base]
@@ -760,6 +823,20 @@ def _(w, i):
     r = ~w.sget(i.ops[1]) & MASK32
     w.sset(i.ops[0], r)
     w.scc = int(r != 0)
+
+
+@op('s_min_u32')
+def _(w, i):
+    a, b = w.sget(i.ops[1]), w.sget(i.ops[2])
+    w.sset(i.ops[0], min(a, b))
+    w.scc = int(a < b)
+
+
+@op('s_max_i32')
+def _(w, i):
+    a, b = sx32(w.sget(i.ops[1])), sx32(w.sget(i.ops[2]))
+    w.sset(i.ops[0], max(a, b))
+    w.scc = int(a > b)
 
 
 @op('s_bitset1_b32')
@@ -1279,6 +1356,102 @@ def _(w, i): w.vset(i.ops[0], w.vget(i.ops[1]).astype(np.float64).view(np.uint64
 
 @op('v_cvt_f32_f64')
 def _(w, i): w.vset(i.ops[0], w.fsrc(i.ops[1], np.float64).astype(np.float32).view(np.uint32))
+
+
+@op('v_rndne_f32')
+def _(w, i): w.vset(i.ops[0], np.rint(w.fsrc(i.ops[1])).astype(np.float32).view(np.uint32))
+
+
+@op('v_sqrt_f32')
+def _(w, i):
+    # correctly rounded (the hardware's is within 1 ulp; the compiler's fixup sequence around it makes either exact)
+    with np.errstate(invalid='ignore'):
+        w.vset(i.ops[0], np.sqrt(w.fsrc(i.ops[1])).astype(np.float32).view(np.uint32))
+
+
+def f32_class(x):
+    """The class bits v_cmp_class tests: 0 sNaN, 1 qNaN, 2 -inf, 3 -normal, 4 -denorm, 5 -0, 6 +0, 7 +denorm,
+    8 +normal, 9 +inf."""
+    u = x.view(np.uint32)
+    neg = (u >> np.uint32(31)).astype(bool)
+    exp = (u >> np.uint32(23)) & np.uint32(255)
+    man = u & np.uint32(0x7FFFFF)
+    cls = np.zeros(x.shape, np.int64)
+    nan = (exp == 255) & (man != 0)
+    cls = np.where(nan & ((man >> np.uint32(22)) == 0), 0, cls)
+    cls = np.where(nan & ((man >> np.uint32(22)) == 1), 1, cls)
+    inf = (exp == 255) & (man == 0)
+    cls = np.where(inf, np.where(neg, 2, 9), cls)
+    norm = (exp > 0) & (exp < 255)
+    cls = np.where(norm, np.where(neg, 3, 8), cls)
+    den = (exp == 0) & (man != 0)
+    cls = np.where(den, np.where(neg, 4, 7), cls)
+    zero = (exp == 0) & (man == 0)
+    cls = np.where(zero, np.where(neg, 5, 6), cls)
+    return cls
+
+
+@op('v_cmp_class_f32')
+def _(w, i):
+    x = w.fsrc(i.ops[1])
+    mask = w.vget(i.ops[2]).astype(np.int64)
+    set_mask(w, i.ops[0], ((mask >> f32_class(x)) & 1).astype(bool))
+
+
+def _f32exp(x):
+    return ((x.view(np.uint32) >> np.uint32(23)) & np.uint32(255)).astype(np.int64)
+
+
+@op('v_div_scale_f32')
+def _(w, i):
+    """Pre-scaling of the correctly rounded division sequence (S0 the value to scale, S1 the denominator, S2 the
+    numerator).  Zero operands give NaN (the final fixup then produces the signed infinity or NaN); the operand
+    ranges that need scaling (denormals, quotients near the overflow or underflow range, tiny numerators) are not
+    modelled and raise."""
+    s0, s1, s2 = (w.fsrc(i.ops[k]) for k in (2, 3, 4))
+    act = w.lanes()
+    zero = (s1 == 0) | (s2 == 0)
+    with np.errstate(all='ignore'):
+        e1, e2 = _f32exp(s1), _f32exp(s2)
+        edge = ~zero & ((e2 - e1 >= 96) | (e1 == 0) | (e2 <= 23) | (np.abs(np.float32(1) / s1) < np.float32(2 ** -126))
+                        | (np.abs(s2 / s1) < np.float32(2 ** -126)) | ~np.isfinite(s1) | ~np.isfinite(s2))
+    if (edge & act).any():
+        raise EmuError('v_div_scale_f32 on operands that need scaling: not modelled')
+    out = np.where(zero, np.float32(np.nan), s0).astype(np.float32)
+    w.vset(i.ops[0], out.view(np.uint32))
+    set_mask(w, i.ops[1], np.zeros(64, bool))
+
+
+@op('v_div_fmas_f32')
+def _(w, i):
+    vcc = (np.uint64(w.s[106] | (w.s[107] << 32)) >> LANES.astype(np.uint64)) & np.uint64(1)
+    if (vcc.astype(bool) & w.lanes()).any():
+        raise EmuError('v_div_fmas_f32 with VCC set (scaled division): not modelled')
+    a, b, c = (w.fsrc(i.ops[k]) for k in (1, 2, 3))
+    w.vset(i.ops[0], exact_fma(a, b, c, np.float32).view(np.uint32))
+
+
+@op('v_div_fixup_f32')
+def _(w, i):
+    q, den, num = (w.fsrc(i.ops[k]) for k in (1, 2, 3))
+    sign = np.signbit(den) ^ np.signbit(num)
+    out = np.where(sign, -np.abs(q), np.abs(q)).astype(np.float32)
+    with np.errstate(all='ignore'):
+        qnan = np.float32(np.nan)
+        out = np.where(np.isnan(num) | np.isnan(den), qnan, out)
+        out = np.where((den == 0) & (num == 0), np.uint32(0xFFC00000).view(np.float32), out)
+        out = np.where(np.isinf(den) & np.isinf(num), np.uint32(0xFFC00000).view(np.float32), out)
+        xinf = ((den == 0) | np.isinf(num)) & ~((den == 0) & (num == 0)) & ~(np.isinf(den) & np.isinf(num)) \
+            & ~np.isnan(num) & ~np.isnan(den)
+        out = np.where(xinf, np.where(sign, -np.inf, np.inf).astype(np.float32), out)
+        xzero = (np.isinf(den) | (num == 0)) & ~xinf & ~((den == 0) & (num == 0)) & \
+            ~(np.isinf(den) & np.isinf(num)) & ~np.isnan(num) & ~np.isnan(den)
+        out = np.where(xzero, np.where(sign, np.float32(-0.0), np.float32(0.0)), out)
+        ordinary = ~(np.isnan(num) | np.isnan(den) | (den == 0) | (num == 0) | np.isinf(den) | np.isinf(num))
+        edge = ordinary & ((_f32exp(num) - _f32exp(den) < -150) | (_f32exp(den) == 255))
+    if (edge & w.lanes()).any():
+        raise EmuError('v_div_fixup_f32 near the underflow or overflow range: not modelled')
+    w.vset(i.ops[0], out.astype(np.float32).view(np.uint32))
 
 
 # --- matrix core

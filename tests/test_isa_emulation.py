@@ -345,3 +345,89 @@ def test_decode_ms_matches_oracle(asm, bits, M, cus):
     got, TS, KS, P = run_decode_ms(asm, mem, lin, N, K, bits, xq, sx, mx, M, cus)
     d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
     assert d is None, (TS, KS, P, d)
+
+
+# ------------------------------------------------------------------ activation quantization and the FFN decode path
+def run_qrow(asm, mem, mode, a, b=None, eps=0.0, w_y=False):
+    """launch_qrow: k_qrow<MODE, EPT> over M rows of n (group mode, 16-byte aligned buffers)."""
+    M, n = a.shape
+    ept = 8 if n <= 8192 else 16 if n <= 16384 else 32
+    threads = ((n // ept + 63) // 64) * 64
+    a_d = mem.alloc(a.nbytes, a)
+    b_d = mem.alloc(b.nbytes, b) if b is not None else 0
+    y = mem.alloc(M * n * 4) if w_y else 0
+    xq, sx, mx = mem.alloc(M * n), mem.alloc(M * 4), mem.alloc(M * (n // 128) * 2)
+    p = E.Program(asm['quant.hip'], f'k_qrowILi{mode}ELi{ept}E')
+    E.launch(p, mem, M, threads, p.pack_args([a_d, b_d, np.float32(eps).view(np.uint32), n, y, xq, sx, mx]))
+    out = (mem.array(xq, np.int8, M * n).reshape(M, n).copy(), mem.array(sx, np.float32, M).copy(),
+           mem.array(mx, np.uint16, M * (n // 128)).reshape(M, n // 128).copy())
+    return out, (mem.array(y, np.float32, M * n).reshape(M, n).copy() if w_y else None)
+
+
+@pytest.fixture(scope='module')
+def qasm():
+    return {src: isa_waits.asm_of(os.path.join(isa_waits.CSRC, src)) for src in ('quant.hip', 'gemm.hip', 'prefill.hip')}
+
+
+def rows_for_quant(seed, M, n):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((M, n)) * rng.choice([1e-3, 1.0, 30.0], (M, 1))).astype(np.float32)
+    x[:, ::97] *= 50                                            # outliers in some groups
+    return x
+
+
+@pytest.mark.parametrize('n', [1024, 2560, 9728])
+def test_qrow_quant(qasm, n):
+    x = rows_for_quant(n, 5, n)
+    mem = E.Memory()
+    (xq, sx, mx), _ = run_qrow(qasm, mem, 0, x)
+    wq_, wsx, wmx = oracle.quant(x)
+    assert (xq == wq_).all() and (sx.view(np.uint32) == wsx.view(np.uint32)).all() and (mx == wmx).all()
+
+
+def test_qrow_rmsnorm_and_silu_mul(qasm):
+    n = 2560
+    x = rows_for_quant(1, 4, n)
+    wgt = (np.random.default_rng(2).standard_normal(n) * 0.1 + 1).astype(np.float32)
+    mem = E.Memory()
+    (xq, sx, mx), _ = run_qrow(qasm, mem, 1, x, wgt, eps=1e-6, w_y=True)
+    wq_, wsx, wmx = oracle.rmsnorm_quant(x, wgt, np.float32(1e-6))
+    assert (xq == wq_).all() and (sx.view(np.uint32) == wsx.view(np.uint32)).all() and (mx == wmx).all()
+    g, u = rows_for_quant(3, 4, n), rows_for_quant(4, 4, n)
+    (xq, sx, mx), _ = run_qrow(qasm, mem, 2, g, u, w_y=True)
+    wq_, wsx, wmx = oracle.silu_mul_quant(g, u)
+    assert (xq == wq_).all() and (sx.view(np.uint32) == wsx.view(np.uint32)).all() and (mx == wmx).all()
+
+
+def test_ffn_decode_path(qasm):
+    """The model runner's one-token FFN step: the gate|up GEMV with silu on the gate half (k_decode<6, 1, SILU0>,
+    output in two parts), then h = silu(g) * u quantized (k_qrow<MUL>) -- equal to det_silu_mul_quant of the
+    oracle's GEMV outputs."""
+    rng = oracle.Rng(70)
+    ff, K, bits = 256, 1024, 6
+    N = 2 * ff
+    rows = rng.fake_rows(bits, N, K)
+    xq, sx, mx = oracle.quant(rng.acts_x(1, K))
+    want = oracle.gemm(rows, N, K, bits, xq, sx, mx)
+    wq_, wsx, wmx = oracle.silu_mul_quant(want[:, :ff], want[:, ff:])
+    mem = E.Memory()
+    wq, c, m = repack(qasm, mem, rows, N, K, bits)
+    T, G = (N + 63) // 64, K // GROUP
+    cus = 4
+    KS = max(1, min((cus + T - 1) // T, (G + 3) // 4)) if 2 * T < cus else 1
+    gs = (G + KS - 1) // KS
+    S = max(1, min((8 * cus + T * KS - 1) // (T * KS), min(gs, 16)))
+    gate, up = mem.alloc(ff * 4), mem.alloc(ff * 4)
+    x_d, sx_d, mx_d = acts(mem, xq, sx, mx)
+    p = E.Program(qasm['gemm.hip'], f'k_decodeILi{bits}ELi1ELb1E')
+    E.launch(p, mem, T * KS, 64 * S,
+             p.pack_args([wq, c, m, N, K, x_d, sx_d, mx_d, 1, out_struct(0, 2, (0, ff, N, 0, 0), (gate, up, 0, 0)),
+                          KS, 0, 0]), dyn_lds=S * 64 * 8 if S > 1 else 0)
+    g_ = mem.array(gate, np.float32, ff).reshape(1, ff).copy()
+    u_ = mem.array(up, np.float32, ff).reshape(1, ff).copy()
+    silu = oracle.lib().ora_silu_f
+    want_g = np.array([[silu(float(v)) for v in want[0, :ff]]], np.float32)
+    assert (g_.view(np.uint32) == want_g.view(np.uint32)).all()
+    assert (u_.view(np.uint32) == want[:, ff:].view(np.uint32)).all()
+    (hq, hs, hm), _ = run_qrow(qasm, mem, 3, g_, u_)
+    assert (hq == wq_).all() and (hs.view(np.uint32) == wsx.view(np.uint32)).all() and (hm == wmx).all()
