@@ -10,7 +10,8 @@ det_convert's output, byte-exact to the converter's restatement on the synthetic
 here a row sample of every quantized tensor kind is re-quantized from the bf16 source by the oracle's quantizer.
 Checked bit for bit: the logits after the 512-token prefill, the logits after each of the first 3 greedy decode
 steps (one token per forward), and the 128 greedy tokens of det_model_generate from the same prompt.
-Progress goes to gpurun_out/test_model_4b.log (the test runs for minutes).
+Progress lines are appended to test_model_4b.log in the output folder that travels back from a GPU run (the test
+runs for minutes).
 """
 import os
 import time
