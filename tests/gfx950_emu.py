@@ -235,7 +235,7 @@ class Program:
         s[0:1] and the workgroup id in s2 as for the library's kernels."""
         p = cls.__new__(cls)
         p.name, p.lds_bytes, p.private_bytes = 'snippet', lds_bytes, private_bytes
-        p.user_sgprs, p.kernarg_size, p.args, p.hidden, p.wg_id_y = 2, 8, [], [], 0
+        p.user_sgprs, p.kernarg_size, p.args, p.hidden, p.wg_id_y, p.wg_id_z = 2, 8, [], [], 0, 0
         p.instrs, labels = [], {}
         for line in lines:
             s = line.split(';')[0].strip()
@@ -253,6 +253,8 @@ class Program:
         for ins in self.instrs:
             if ins.mn.startswith(('s_branch', 's_cbranch')):
                 ins.target = labels[ins.ops[0]]
+            elif ins.mn == 's_set_gpr_idx_on':
+                ins.ops = [Op(ins.ops[0])]          # the gpr_idx(...) list is read from the text
             else:
                 ins.ops = [Op(o) for o in ins.ops]
             ins.fn = handler(ins.mn)
@@ -282,9 +284,9 @@ class Program:
         self.private_bytes = int(d['amdhsa_private_segment_fixed_size'])
         self.user_sgprs = int(d['amdhsa_user_sgpr_count'])
         self.wg_id_y = int(d.get('amdhsa_system_sgpr_workgroup_id_y', 0))
+        self.wg_id_z = int(d.get('amdhsa_system_sgpr_workgroup_id_z', 0))
         for k in ('amdhsa_user_sgpr_dispatch_ptr', 'amdhsa_user_sgpr_queue_ptr', 'amdhsa_user_sgpr_dispatch_id',
-                  'amdhsa_user_sgpr_kernarg_preload_length', 'amdhsa_system_sgpr_workgroup_id_z',
-                  'amdhsa_system_sgpr_workgroup_info'):
+                  'amdhsa_user_sgpr_kernarg_preload_length', 'amdhsa_system_sgpr_workgroup_info'):
             if int(d.get(k, 0)):
                 raise EmuError(f'{k} is not modelled')
         if not int(d['amdhsa_user_sgpr_kernarg_segment_ptr']) or self.user_sgprs != 2:
@@ -336,6 +338,7 @@ class Wave:
         self.queue = []                 # pending vector-memory operations, oldest first
         self.pending_v = {}             # vgpr -> count of pending writes
         self.priv = np.zeros((64, max(program.private_bytes, 4) + 64), np.uint8)
+        self.gpr_idx = None
 
     # --- scalar access
     def sget(self, op, width=1):
@@ -605,6 +608,8 @@ def _dpp(w, i):
     elif base == 'v_max_f32':
         r = np.fmax(vals.view(np.float32), w.fsrc(i.ops[2])).astype(np.float32)
         w.vset(i.ops[0], r.view(np.uint32), mask=write)
+    elif base == 'v_add_u32':
+        w.vset(i.ops[0], (vals.astype(np.uint64) + w.vget(i.ops[2]).astype(np.uint64)).astype(np.uint32), mask=write)
     else:
         raise EmuError(f'{i.mn} not modelled')
 
@@ -633,7 +638,7 @@ def handler(mn):
         return _sdwa
     if mn == 'v_cvt_i32_f32_sdwa':
         return _cvt_sdwa
-    if mn.endswith('_dpp') and mn[:-4] in ('v_mov_b32', 'v_add_f32', 'v_max_f32'):
+    if mn.endswith('_dpp') and mn[:-4] in ('v_mov_b32', 'v_add_f32', 'v_max_f32', 'v_add_u32'):
         return _dpp
     base = re.sub(r'_e(32|64)$', '', mn)
     if base in H:
@@ -839,6 +844,18 @@ def _(w, i):
     w.scc = int(a > b)
 
 
+@op('s_ff1_i32_b64')
+def _(w, i):
+    v = w.sget(i.ops[1], 2)
+    w.sset(i.ops[0], ((v & -v).bit_length() - 1) & MASK32 if v else MASK32)
+
+
+@op('s_flbit_i32_b64')
+def _(w, i):
+    v = w.sget(i.ops[1], 2)
+    w.sset(i.ops[0], 64 - v.bit_length() if v else MASK32)
+
+
 @op('s_bitset1_b32')
 def _(w, i): w.sset(i.ops[0], w.sget(i.ops[0]) | (1 << (w.sget(i.ops[1]) & 31)))
 
@@ -901,6 +918,18 @@ H['s_andn2_saveexec_b64'] = _saveexec(lambda s, e: s & ~e)
 
 @op('s_nop', 's_setprio', 's_sleep')
 def _(w, i): pass
+
+
+@op('s_set_gpr_idx_on')
+def _(w, i):
+    """VGPR index mode: the operands named in gpr_idx(...) of the following vector instructions are offset by the
+    index (the SGPR's low 8 bits) until s_set_gpr_idx_off."""
+    m = re.search(r'gpr_idx\(([^)]*)\)', i.text)
+    w.gpr_idx = (w.sget(i.ops[0]) & 0xFF, {x.strip() for x in m.group(1).split(',')})
+
+
+@op('s_set_gpr_idx_off')
+def _(w, i): w.gpr_idx = None
 
 
 @op('s_waitcnt')
@@ -1009,6 +1038,47 @@ H['v_lshlrev_b16'] = _v16(lambda a, b: b << (a & np.uint64(15)))
 H['v_lshrrev_b16'] = _v16(lambda a, b: b >> (a & np.uint64(15)))
 
 
+@op('v_not_b32')
+def _(w, i): w.vset(i.ops[0], ~w.vget(i.ops[1]))
+
+
+@op('v_bfrev_b32')
+def _(w, i):
+    a = w.vget(i.ops[1])
+    r = np.zeros(64, np.uint32)
+    for b in range(32):
+        r |= ((a >> np.uint32(b)) & np.uint32(1)) << np.uint32(31 - b)
+    w.vset(i.ops[0], r)
+
+
+@op('v_bfe_i32')
+def _(w, i):
+    a = w.vget(i.ops[1]).astype(np.int64)
+    off = (w.vget(i.ops[2]) & np.uint32(31)).astype(np.int64)
+    wd = (w.vget(i.ops[3]) & np.uint32(31)).astype(np.int64)
+    x = (a >> off) & ((np.int64(1) << wd) - 1)
+    sgn = (wd > 0) & ((x >> np.maximum(wd - 1, 0)) & 1).astype(bool)
+    x = np.where(sgn, x - (np.int64(1) << wd), x)
+    w.vset(i.ops[0], (x & MASK32).astype(np.uint32))
+
+
+@op('v_med3_i32')
+def _(w, i):
+    a, b, c = (i32(w.vget(i.ops[k])).astype(np.int64) for k in (1, 2, 3))
+    w.vset(i.ops[0], np.median(np.stack([a, b, c]), axis=0).astype(np.int64).astype(np.int32).view(np.uint32))
+
+
+@op('v_ffbh_i32')
+def _(w, i):
+    # first bit that differs from the sign bit, counted from the MSB; -1 (0xffffffff) for 0 and -1
+    a = i32(w.vget(i.ops[1])).astype(np.int64)
+    x = np.where(a < 0, ~a, a) & MASK32
+    r = np.full(64, MASK32, np.uint64)
+    nz = x != 0
+    r[nz] = np.array([32 - int(v).bit_length() for v in x[nz]], np.uint64)
+    w.vset(i.ops[0], r)
+
+
 @op('v_ashrrev_i32')
 def _(w, i):
     a, b = w.vget(i.ops[1]), i32(w.vget(i.ops[2]))
@@ -1081,6 +1151,18 @@ def _(w, i):
             tc = c if idx & 1 else ~c
             out |= ta & tb & tc
     w.vset(i.ops[0], out)
+
+
+@op('v_bitop3_b16')
+def _(w, i):
+    # the low halves; the high half of the destination is written as zero (16-bit ops of the gfx9 family)
+    a, b, c = (w.vget(i.ops[k]) & np.uint32(0xFFFF) for k in (1, 2, 3))
+    lut = parse_int(str(i.mods['bitop3']))
+    out = np.zeros(64, np.uint32)
+    for idx in range(8):
+        if lut >> idx & 1:
+            out |= (a if idx & 4 else ~a) & (b if idx & 2 else ~b) & (c if idx & 1 else ~c)
+    w.vset(i.ops[0], out & np.uint32(0xFFFF))
 
 
 @op('v_mbcnt_lo_u32_b32', 'v_mbcnt_hi_u32_b32')
@@ -1266,6 +1348,41 @@ H['v_max_f32'] = _f2(np.fmax)
 H['v_min_f32'] = _f2(np.fmin)
 
 
+H['v_add_f64'] = _f2(lambda a, b: a + b, np.float64)
+H['v_mul_f64'] = _f2(lambda a, b: a * b, np.float64)
+H['v_max_f64'] = _f2(np.fmax, np.float64)
+H['v_min_f64'] = _f2(np.fmin, np.float64)
+H['v_subrev_f32'] = _f2(lambda a, b: b - a)
+
+
+@op('v_cvt_f64_f32')
+def _(w, i): w.vset(i.ops[0], w.fsrc(i.ops[1]).astype(np.float64).view(np.uint64), 2)
+
+
+@op('v_rndne_f64')
+def _(w, i): w.vset(i.ops[0], np.rint(w.fsrc(i.ops[1], np.float64)).view(np.uint64), 2)
+
+
+@op('v_rcp_f64')
+def _(w, i):
+    with np.errstate(all='ignore'):
+        w.vset(i.ops[0], (1.0 / w.fsrc(i.ops[1], np.float64)).view(np.uint64), 2)
+
+
+@op('v_cvt_i32_f64')
+def _(w, i):
+    x = w.fsrc(i.ops[1], np.float64)
+    x = np.where(np.isnan(x), 0, np.clip(np.trunc(x), -2 ** 31, 2 ** 31 - 1))
+    w.vset(i.ops[0], x.astype(np.int64).astype(np.int32).view(np.uint32))
+
+
+@op('v_cvt_u32_f64')
+def _(w, i):
+    x = w.fsrc(i.ops[1], np.float64)
+    x = np.where(np.isnan(x), 0, np.clip(np.trunc(x), 0, MASK32))
+    w.vset(i.ops[0], x.astype(np.uint64).astype(np.uint32))
+
+
 @op('v_fmac_f32', 'v_fmac_f64')
 def _(w, i):
     dt = np.float32 if i.mn.endswith('f32') else np.float64
@@ -1431,27 +1548,68 @@ def _(w, i):
     w.vset(i.ops[0], exact_fma(a, b, c, np.float32).view(np.uint32))
 
 
-@op('v_div_fixup_f32')
-def _(w, i):
-    q, den, num = (w.fsrc(i.ops[k]) for k in (1, 2, 3))
+def _div_fixup(w, i, dt):
+    """Special cases of the division sequence's final step (the instruction set reference's table): NaN operands,
+    0/0 and inf/inf give the default NaN; x/0 and inf/y a signed infinity; x/inf and 0/y a signed zero; otherwise
+    the quotient with the sign of num/den.  Quotients that would underflow or overflow raise (not modelled)."""
+    q, den, num = (w.fsrc(i.ops[k], dt) for k in (1, 2, 3))
     sign = np.signbit(den) ^ np.signbit(num)
-    out = np.where(sign, -np.abs(q), np.abs(q)).astype(np.float32)
+    out = np.where(sign, -np.abs(q), np.abs(q)).astype(dt)
+    qnan = np.array([0xFFC00000], np.uint32).view(np.float32)[0] if dt == np.float32 else \
+        np.array([0xFFF8000000000000], np.uint64).view(np.float64)[0]
+    nan = np.isnan(num) | np.isnan(den)
+    zz = (den == 0) & (num == 0)
+    ii = np.isinf(den) & np.isinf(num)
+    xinf = ((den == 0) | np.isinf(num)) & ~zz & ~ii & ~nan
+    xzero = (np.isinf(den) | (num == 0)) & ~xinf & ~zz & ~ii & ~nan
+    out = np.where(xzero, np.where(sign, dt(-0.0), dt(0.0)), out)
+    out = np.where(xinf, np.where(sign, dt(-np.inf), dt(np.inf)), out)
+    out = np.where(zz | ii, qnan, out)
+    out = np.where(np.isnan(num), num, np.where(np.isnan(den), den, out))
+    ordinary = ~(nan | (den == 0) | (num == 0) | np.isinf(den) | np.isinf(num))
+    ex = _f32exp if dt == np.float32 else _f64exp
+    lo, top = (-150, 255) if dt == np.float32 else (-1075, 2047)
     with np.errstate(all='ignore'):
-        qnan = np.float32(np.nan)
-        out = np.where(np.isnan(num) | np.isnan(den), qnan, out)
-        out = np.where((den == 0) & (num == 0), np.uint32(0xFFC00000).view(np.float32), out)
-        out = np.where(np.isinf(den) & np.isinf(num), np.uint32(0xFFC00000).view(np.float32), out)
-        xinf = ((den == 0) | np.isinf(num)) & ~((den == 0) & (num == 0)) & ~(np.isinf(den) & np.isinf(num)) \
-            & ~np.isnan(num) & ~np.isnan(den)
-        out = np.where(xinf, np.where(sign, -np.inf, np.inf).astype(np.float32), out)
-        xzero = (np.isinf(den) | (num == 0)) & ~xinf & ~((den == 0) & (num == 0)) & \
-            ~(np.isinf(den) & np.isinf(num)) & ~np.isnan(num) & ~np.isnan(den)
-        out = np.where(xzero, np.where(sign, np.float32(-0.0), np.float32(0.0)), out)
-        ordinary = ~(np.isnan(num) | np.isnan(den) | (den == 0) | (num == 0) | np.isinf(den) | np.isinf(num))
-        edge = ordinary & ((_f32exp(num) - _f32exp(den) < -150) | (_f32exp(den) == 255))
+        edge = ordinary & ((ex(num) - ex(den) < lo) | (ex(den) == top))
     if (edge & w.lanes()).any():
-        raise EmuError('v_div_fixup_f32 near the underflow or overflow range: not modelled')
-    w.vset(i.ops[0], out.astype(np.float32).view(np.uint32))
+        raise EmuError('division fixup near the underflow or overflow range: not modelled')
+    w.vset(i.ops[0], out.astype(dt).view(np.uint32 if dt == np.float32 else np.uint64), 1 if dt == np.float32 else 2)
+
+
+@op('v_div_fixup_f32')
+def _(w, i): _div_fixup(w, i, np.float32)
+
+
+def _f64exp(x):
+    return ((x.view(np.uint64) >> np.uint64(52)) & np.uint64(0x7FF)).astype(np.int64)
+
+
+@op('v_div_scale_f64')
+def _(w, i):
+    s0, s1, s2 = (w.fsrc(i.ops[k], np.float64) for k in (2, 3, 4))
+    act = w.lanes()
+    zero = (s1 == 0) | (s2 == 0)
+    with np.errstate(all='ignore'):
+        e1, e2 = _f64exp(s1), _f64exp(s2)
+        edge = ~zero & ((e2 - e1 >= 768) | (e1 == 0) | (e2 <= 53) | (np.abs(1.0 / s1) < 2.0 ** -1022)
+                        | (np.abs(s2 / s1) < 2.0 ** -1022) | ~np.isfinite(s1) | ~np.isfinite(s2))
+    if (edge & act).any():
+        raise EmuError('v_div_scale_f64 on operands that need scaling: not modelled')
+    w.vset(i.ops[0], np.where(zero, np.nan, s0).view(np.uint64), 2)
+    set_mask(w, i.ops[1], np.zeros(64, bool))
+
+
+@op('v_div_fmas_f64')
+def _(w, i):
+    vcc = (np.uint64(w.s[106] | (w.s[107] << 32)) >> LANES.astype(np.uint64)) & np.uint64(1)
+    if (vcc.astype(bool) & w.lanes()).any():
+        raise EmuError('v_div_fmas_f64 with VCC set (scaled division): not modelled')
+    a, b, c = (w.fsrc(i.ops[k], np.float64) for k in (1, 2, 3))
+    w.vset(i.ops[0], exact_fma(a, b, c, np.float64).view(np.uint64), 2)
+
+
+@op('v_div_fixup_f64')
+def _(w, i): _div_fixup(w, i, np.float64)
 
 
 # --- matrix core
@@ -1483,6 +1641,35 @@ def _(w, i):
     out[_MF_DLANE, _MF_DREG] = D
     w.check_v(d.base, 16, 'writes')
     w.v[d.base:d.base + 16] = out.T
+
+
+# v_mfma_i32_16x16x64_i8: operand element (row or column r, k) in lane r + 16 (k // 16), byte k % 16; result element
+# (i, j) in lane j + 16 (i // 4), register i % 4
+_M16_R, _M16_K = np.meshgrid(np.arange(16), np.arange(64), indexing='ij')
+_M16_LANE, _M16_BYTE = _M16_R + 16 * (_M16_K // 16), _M16_K % 16
+_M16_I, _M16_J = np.meshgrid(np.arange(16), np.arange(16), indexing='ij')
+_M16_DLANE, _M16_DREG = _M16_J + 16 * (_M16_I // 4), _M16_I % 4
+
+
+@op('v_mfma_i32_16x16x64_i8')
+def _(w, i):
+    d, a, b, c = i.ops
+    w.check_v(a.base, 4, 'reads')
+    w.check_v(b.base, 4, 'reads')
+    A = w.v[a.base:a.base + 4].T.copy().view(np.int8).reshape(64, 16)
+    B = w.v[b.base:b.base + 4].T.copy().view(np.int8).reshape(64, 16)
+    Am = A[_M16_LANE, _M16_BYTE].astype(np.int64)               # [row][k]
+    Bm = B[_M16_LANE, _M16_BYTE].astype(np.int64).T             # [k][col]
+    if c.kind == 'lit':
+        Cm = np.full((16, 16), c.value, np.int64)
+    else:
+        w.check_v(c.base, 4, 'reads')
+        Cm = w.v[c.base:c.base + 4].T.view(np.int32)[_M16_DLANE, _M16_DREG].astype(np.int64)
+    D = ((Am @ Bm + Cm) & MASK32).astype(np.uint32)
+    out = np.zeros((64, 4), np.uint32)
+    out[_M16_DLANE, _M16_DREG] = D
+    w.check_v(d.base, 4, 'writes')
+    w.v[d.base:d.base + 4] = out.T
 
 
 @op('v_dot4c_i32_i8')
@@ -1518,6 +1705,27 @@ def _(w, i):
         return
     w.check_v(i.ops[0].base, size // 4, 'writes')
     w.vset_regs(i.ops[0].base, data.view(np.uint32).reshape(64, size // 4), act)
+
+
+@op('ds_read2st64_b32')
+def _(w, i):
+    act = w.lanes()
+    addr = _ds_addr(w, i.ops[1])
+    out = np.zeros((64, 2), np.uint32)
+    for k, key in enumerate(('offset0', 'offset1')):
+        out[:, k] = w.wg.lds_read(addr + int(i.mods.get(key, 0)) * 256, 4, act, w).view(np.uint32).reshape(64)
+    w.check_v(i.ops[0].base, 2, 'writes')
+    w.vset_regs(i.ops[0].base, out, act)
+
+
+@op('ds_write2st64_b32', 'ds_write2_b32')
+def _(w, i):
+    act = w.lanes()
+    addr = _ds_addr(w, i.ops[0])
+    unit = 256 if 'st64' in i.mn else 4
+    for k, key in enumerate(('offset0', 'offset1')):
+        data = w.vget(i.ops[1 + k]).view(np.uint8).reshape(64, 4)
+        w.wg.lds_write(addr + int(i.mods.get(key, 0)) * unit, data, act, w)
 
 
 @op('ds_read2st64_b64', 'ds_read2_b64')
@@ -1656,10 +1864,11 @@ def _(w, i):
     issue_load(w, i.ops[0].base, arr, act)
 
 
-@op('global_store_dword', 'global_store_dwordx2', 'global_store_dwordx4', 'global_store_short', 'global_store_byte')
+@op('global_store_dword', 'global_store_dwordx2', 'global_store_dwordx3', 'global_store_dwordx4', 'global_store_short',
+    'global_store_byte')
 def _(w, i):
-    size = {'global_store_dword': 4, 'global_store_dwordx2': 8, 'global_store_dwordx4': 16, 'global_store_short': 2,
-            'global_store_byte': 1}[i.mn]
+    size = {'global_store_dword': 4, 'global_store_dwordx2': 8, 'global_store_dwordx3': 12, 'global_store_dwordx4': 16,
+            'global_store_short': 2, 'global_store_byte': 1}[i.mn]
     addr, act = _gaddr(w, i, i.ops[0], i.ops[2])
     nreg = max(1, size // 4)
     w.check_v(i.ops[1].base, nreg, 'reads')
@@ -1687,6 +1896,48 @@ def _(w, i):
         issue_load(w, vdst.base, old.reshape(64, 1), act)
     else:
         w.queue.append(Pending())
+
+
+@op('global_atomic_umax', 'global_atomic_umax_x2')
+def _(w, i):
+    wide = i.mn.endswith('_x2')
+    n = 8 if wide else 4
+    ret = 'sc0' in i.mods or 'glc' in i.mods
+    if ret:
+        vdst, vaddr, vdata, saddr = i.ops
+    else:
+        vaddr, vdata, saddr = i.ops
+    addr, act = _gaddr(w, i, vaddr, saddr)
+    val = w.vget(vdata, 2 if wide else 1)
+    dt = np.uint64 if wide else np.uint32
+    old = np.zeros((64, n // 4), np.uint32)
+    for l in np.nonzero(act)[0]:                 # lanes in order: max commutes
+        a = int(addr[l])
+        o = int(w.wg.mem.read(a, n).view(dt)[0])
+        old[l] = np.array([o], dt).view(np.uint32)
+        w.wg.mem.write(a, np.array([max(o, int(val[l]))], dt).view(np.uint8))
+    if ret:
+        issue_load(w, vdst.base, old, act)
+    else:
+        w.queue.append(Pending())
+
+
+@op('flat_load_dword', 'flat_load_dwordx2', 'flat_load_dwordx4')
+def _(w, i):
+    """Generic addresses: the LDS aperture (src_shared_base's high word) reads LDS, anything else device memory."""
+    n = int(i.mn[-1]) if i.mn[-2] == 'x' else 1
+    act = w.lanes()
+    addr = w.vget(i.ops[1], 2).astype(np.int64) + parse_int(str(i.mods.get('offset', 0)))
+    lds = ((addr >> 32) == 0x10000) & act
+    if (((addr >> 32) == 0x20000) & act).any():
+        raise EmuError('flat access to scratch is not modelled')
+    data = np.zeros((64, 4 * n), np.uint8)
+    if lds.any():
+        data[lds] = w.wg.lds_read(addr & MASK32, 4 * n, lds, w)[lds]
+    glob = act & ~lds
+    if glob.any():
+        data[glob] = w.wg.mem.gather(addr, 4 * n, glob)[glob]
+    issue_load(w, i.ops[0].base, data.view(np.uint32).reshape(64, n), act)
 
 
 @op('global_atomic_add_x2', 'global_atomic_swap_x2')
@@ -1746,7 +1997,7 @@ def _scratch_off(w, i, vaddr, saddr):
 
 # ------------------------------------------------------------------------------------------------ workgroups
 class Workgroup:
-    def __init__(self, prog, mem, wg_id, nthreads, wg_id_y=0, dyn_lds=0):
+    def __init__(self, prog, mem, wg_id, nthreads, wg_id_y=0, dyn_lds=0, wg_id_z=0):
         self.prog, self.mem = prog, mem
         self.lds_size = prog.lds_bytes + dyn_lds
         self.lds = np.zeros(max(self.lds_size, 4) + 16, np.uint8)
@@ -1756,8 +2007,12 @@ class Workgroup:
             w = Wave(self, wv, prog)
             w.s[0], w.s[1] = KERNARG & MASK32, KERNARG >> 32
             w.s[2] = wg_id
+            k = 3
             if prog.wg_id_y:
-                w.s[3] = wg_id_y
+                w.s[k] = wg_id_y
+                k += 1
+            if prog.wg_id_z:
+                w.s[k] = wg_id_z
             tid = wv * 64 + LANES
             w.v[0] = tid.astype(np.uint32)
             n = min(64, nthreads - wv * 64)
@@ -1815,6 +2070,8 @@ class Workgroup:
             for w in live:
                 while not w.done and not w.at_barrier:
                     ins = self.prog.instrs[w.pc]
+                    if w.gpr_idx is not None and ins.mn.startswith('v_'):
+                        ins = indexed(ins, *w.gpr_idx)
                     try:
                         ins.fn(w, ins)
                     except EmuError as e:
@@ -1838,6 +2095,22 @@ class Workgroup:
                 raise EmuError('deadlock: waves wait at a barrier that others never reach')
 
 
+def indexed(ins, idx, which):
+    """A copy of a vector instruction with the index added to the VGPR operands that index mode names."""
+    pos = {'DST': 0, 'SRC0': 1, 'SRC1': 2, 'SRC2': 3}
+    new = Instr.__new__(Instr)
+    new.mn, new.mods, new.text, new.fn, new.target = ins.mn, ins.mods, ins.text + f' [index {idx}]', ins.fn, ins.target
+    new.ops = list(ins.ops)
+    for name in which:
+        k = pos[name]
+        o = new.ops[k]
+        if o.kind == 'v':
+            c = Op(o.text)
+            c.base = o.base + idx
+            new.ops[k] = c
+    return new
+
+
 KERNARG = 0x7E0000000000
 TRACE = None          # debugging hook: called with (wave, instruction) after each instruction
 
@@ -1855,20 +2128,23 @@ def launch(prog, mem, grid, block, kernarg_bytes, dyn_lds=0):
         raise EmuError('kernel arguments larger than the kernel expects')
     ka = np.zeros(max(prog.kernarg_size, 8) + 64, np.uint8)
     ka[:len(kernarg_bytes)] = np.frombuffer(bytes(kernarg_bytes), np.uint8)
-    gx, gy = (grid, 1) if isinstance(grid, int) else grid
-    if gy > 1 and not prog.wg_id_y:
-        raise EmuError('a 2-D grid for a kernel that does not read its y workgroup id')
+    gx, gy, gz = (grid, 1, 1) if isinstance(grid, int) else (tuple(grid) + (1, 1))[:3]
+    if (gy > 1 and not prog.wg_id_y) or (gz > 1 and not prog.wg_id_z):
+        raise EmuError('a grid dimension the kernel does not read')
     for off, size, kind in prog.hidden:        # launch dimensions; every other hidden argument (queues, heaps) is 0
         v = HIDDEN[kind](gx, block) if kind in HIDDEN else 0
         if kind == 'hidden_block_count_y':
             v = gy
+        if kind == 'hidden_block_count_z':
+            v = gz
         if kind == 'hidden_dynamic_lds_size':
             v = dyn_lds
         ka[off:off + size] = np.frombuffer(int(v).to_bytes(size, 'little'), np.uint8)
     mem.bufs = [b for b in mem.bufs if b[0] != KERNARG]
     mem.bufs.append((KERNARG, ka))
     steps = 0
-    for y in range(gy):
-        for x in range(gx):
-            steps += Workgroup(prog, mem, x, block, y, dyn_lds).run()
+    for z in range(gz):
+        for y in range(gy):
+            for x in range(gx):
+                steps += Workgroup(prog, mem, x, block, y, dyn_lds, z).run()
     return steps

@@ -431,3 +431,24 @@ def test_ffn_decode_path(qasm):
     assert (u_.view(np.uint32) == want[:, ff:].view(np.uint32)).all()
     (hq, hs, hm), _ = run_qrow(qasm, mem, 3, g_, u_)
     assert (hq == wq_).all() and (hs.view(np.uint32) == wsx.view(np.uint32)).all() and (hm == wmx).all()
+
+
+# ------------------------------------------------------------------ det convert's weight quantizer
+@pytest.mark.parametrize('bits', [4, 6, 8])
+def test_quantize_rows(qasm, bits):
+    """k_quantize (binary64 scale search, indexed-register code packing) against the oracle's quantize_rows, byte for
+    byte, on Gaussian rows with a zero group, a scaled group and a single outlier."""
+    rng = np.random.default_rng(80 + bits)
+    N, K = 6, 512
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w[1, 128:256] = 0
+    w[2, :128] *= 1e-3
+    w[3, 300] = 1.5
+    mem = E.Memory()
+    w_d = mem.alloc(w.nbytes, w)
+    rb = K // 32 * BPL[bits] + 4 + 2 * (K // GROUP)
+    out = mem.alloc(N * rb)
+    p = E.Program(qasm['gemm.hip'], 'k_quantizeEPKfiiPh')
+    E.launch(p, mem, N, 64, p.pack_args([w_d, K, bits, out]))
+    got = mem.array(out, np.uint8, N * rb).reshape(N, rb)
+    assert (got == oracle.quantize_rows(w, bits)).all()
