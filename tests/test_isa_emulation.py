@@ -452,3 +452,206 @@ def test_quantize_rows(qasm, bits):
     E.launch(p, mem, N, 64, p.pack_args([w_d, K, bits, out]))
     got = mem.array(out, np.uint8, N * rb).reshape(N, rb)
     assert (got == oracle.quantize_rows(w, bits)).all()
+
+
+# ------------------------------------------------------------------ token mixers
+@pytest.fixture(scope='module')
+def masm():
+    return {'mixer.hip': isa_waits.asm_of(os.path.join(isa_waits.CSRC, 'mixer.hip'))}
+
+
+def test_argmax(masm):
+    """k_argmax_part + k_argmax_fin: the first of tied maxima, NaN skipped (a NaN first element gives 0), -0 == +0,
+    over several 2048-value slices; the row accumulators are left at zero."""
+    rng = np.random.default_rng(5)
+    V = 5000
+    x = rng.standard_normal((5, V)).astype(np.float32)
+    x[0, [17, 4000]] = 9.0                                   # tie across slices: the first wins
+    x[1, :] = np.nan
+    x[1, 3000] = 1.0
+    x[2, :] = -0.0
+    x[2, 7] = 0.0                                            # all zeros: index 0
+    x[3, 0] = np.nan                                         # a NaN first element reads as 0
+    x[4, 2047], x[4, 2048] = 5.0, 5.0                        # tie at the slice boundary
+    want = [int(oracle.lib().ora_argmax(P_(row), V)) for row in x]
+    mem = E.Memory()
+    l_d = mem.alloc(x.nbytes, x)
+    acc = mem.alloc(256 * 8)
+    out = mem.alloc(5 * 4)
+    p = E.Program(masm['mixer.hip'], 'k_argmax_part')
+    E.launch(p, mem, ((V + 2047) // 2048, 5), 256, p.pack_args([l_d, V, acc]))
+    p = E.Program(masm['mixer.hip'], 'k_argmax_fin')
+    E.launch(p, mem, 1, 256, p.pack_args([l_d, 5, V, acc, out]))
+    assert mem.array(out, np.int32, 5).tolist() == want
+    assert (mem.array(acc, np.uint64, 5) == 0).all()
+
+
+def P_(a):
+    import ctypes
+    return np.ascontiguousarray(a).ctypes.data_as(ctypes.c_void_p)
+
+
+def rope_tables(cap, half, theta=10000000.0):
+    pos = np.arange(cap, dtype=np.float64)[:, None]
+    inv = 1.0 / theta ** (np.arange(half, dtype=np.float64) / max(half, 1))
+    return np.cos(pos * inv).astype(np.float32), np.sin(pos * inv).astype(np.float32)
+
+
+def f32bits(x):
+    return int(np.float32(x).view(np.uint32))
+
+
+def attn_scratch(mem, M, n_h, hd):
+    """attn_layout: qq, sq, mxo, den, num, cnt (256-byte aligned) in one zeroed block; the struct passed by value."""
+    al = lambda b: (b + 255) & ~255
+    r = M * n_h
+    sizes = [al(r * hd), al(r * 4), al(r * 4), al(r * 8), al(r * hd * 8), al(r * 4)]
+    base = mem.alloc(sum(sizes))
+    ptrs, off = [], 0
+    for sz in sizes:
+        ptrs.append(base + off)
+        off += sz
+    return b''.join(int(p).to_bytes(8, 'little') for p in ptrs) + int(off).to_bytes(8, 'little')
+
+
+def emulate_attention(asm, mem, dev, M, pos0, n_h, n_kv, hd, rot, eps, qg_d, k_d, v_d, o_d):
+    """det_attention's launches (mixer.hip), for the paths these shapes take."""
+    S = attn_scratch(mem, M, n_h, hd)
+    nrows, half = M * (n_kv + n_h), rot // 2
+    ept = {256: 4, 128: 2, 64: 1}.get(hd, 0)
+    assert ept and half % ept == 0
+    p = E.Program(asm, f'k_attn_prep_wILi{ept}E')
+    E.launch(p, mem, (nrows + 3) // 4, 256, p.pack_args([
+        dev['kn'], dev['vi'], dev['kq'], dev['sk'], dev['vq'], k_d, v_d, dev['qn'], qg_d, dev['cos'], dev['sin'], half,
+        f32bits(eps), pos0, n_kv, n_h, M * n_kv, nrows, S]))
+    nkeys = pos0 + M
+    if M <= 4:
+        grid = ((nkeys + 31) // 32, M * n_h)
+        p = E.Program(asm, 'k_attn_maxILi32E')
+        E.launch(p, mem, grid, 256, p.pack_args([dev['kq'], dev['sk'], pos0, n_h, n_kv, hd, S]))
+        p = E.Program(asm, 'k_attn_accILi32ELb1E')
+        E.launch(p, mem, grid, 256, p.pack_args([dev['kq'], dev['sk'], dev['vq'], pos0, n_h, n_kv, hd, S, dev['vs'],
+                                                 qg_d, o_d]))
+    else:
+        assert hd in (64, 128, 256)
+        rep = n_h // n_kv
+        grid = (hd // 32, (M + 15) // 16, n_kv * ((rep + 3) // 4))
+        p = E.Program(asm, f'k_attn_mmaILi{hd}E')
+        E.launch(p, mem, grid, 256, p.pack_args([dev['kq'], dev['sk'], dev['vq'], pos0, M, n_h, n_kv, S, dev['vs'],
+                                                 qg_d, o_d]))
+
+
+def test_attention_prefill_then_decode(masm):
+    """Head dim 256 with 64 rotary dims and 4 q heads per kv head, as in the 4B model: a 20-token batch on the matrix
+    cores, then two single-token steps over 32-key chunks; outputs and the KV cache rows against the oracle."""
+    import ctypes
+    n_h, n_kv, hd, rot, cap = 8, 2, 256, 64, 32
+    rng = np.random.default_rng(1)
+    f32 = np.float32
+    q_norm = (1 + 0.2 * rng.standard_normal(hd)).astype(f32)
+    k_norm = (1 + 0.2 * rng.standard_normal(hd)).astype(f32)
+    v_scale = np.array([1 / 1024, 1 / 256][:n_kv], f32)
+    v_inv = (f32(1) / v_scale).astype(f32)
+    cos, sin = rope_tables(cap, rot // 2)
+    mem = E.Memory()
+    dev = {n: mem.alloc(a.nbytes, a) for n, a in (('qn', q_norm), ('kn', k_norm), ('vs', v_scale), ('vi', v_inv),
+                                                  ('cos', cos), ('sin', sin))}
+    dev['kq'], dev['sk'], dev['vq'] = mem.alloc(cap * n_kv * hd), mem.alloc(cap * n_kv * 4), mem.alloc(cap * n_kv * hd * 2)
+    kq, sk, vq = np.zeros((cap, n_kv, hd), np.int8), np.zeros((cap, n_kv), f32), np.zeros((cap, n_kv, hd), np.int16)
+    L = oracle.lib()
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    pos = 0
+    for M in (20, 1, 1):
+        qg = rng.standard_normal((M, n_h, 2 * hd)).astype(f32)
+        k = rng.standard_normal((M, n_kv, hd)).astype(f32)
+        v = (rng.standard_normal((M, n_kv, hd)) * 0.05).astype(f32)
+        qg_d, k_d, v_d = (mem.alloc(a.nbytes, a) for a in (qg, k, v))
+        o_d = mem.alloc(M * n_h * hd * 4)
+        emulate_attention(masm['mixer.hip'], mem, dev, M, pos, n_h, n_kv, hd, rot, 1e-6, qg_d, k_d, v_d, o_d)
+        o = np.zeros((M, n_h, hd), f32)
+        L.ora_attention(ptr(q_norm), ptr(k_norm), ptr(v_scale), ptr(v_inv), ptr(kq), ptr(sk), ptr(vq), ptr(qg), ptr(k),
+                        ptr(v), ptr(cos), ptr(sin), rot, f32(1e-6), M, pos, n_h, n_kv, hd, ptr(o))
+        got = mem.array(o_d, np.float32, M * n_h * hd).reshape(M, n_h, hd)
+        assert (got.view(np.uint32) == o.view(np.uint32)).all(), f'o at M={M} pos0={pos}'
+        pos += M
+        assert (mem.array(dev['kq'], np.int8, cap * n_kv * hd).reshape(cap, n_kv, hd)[:pos] == kq[:pos]).all()
+        assert (mem.array(dev['sk'], np.uint32, cap * n_kv).reshape(cap, n_kv)[:pos] == sk[:pos].view(np.uint32)).all()
+        assert (mem.array(dev['vq'], np.int16, cap * n_kv * hd).reshape(cap, n_kv, hd)[:pos] == vq[:pos]).all()
+
+
+def emulate_gdn(asm, mem, dev, M, n_k, n_v, dk, dv, eps, qkv_d, z_d, a_d, b_d, on_d):
+    """gdn_run's launches (mixer.hip) without the fused a|b projection."""
+    cd = 2 * n_k * dk + n_v * dv
+    nfl = M * cd + 2 * M * n_k * dk + 2 * M * n_v + M * n_v * dv + n_v
+    scratch = mem.alloc(nfl * 4)
+    y = scratch
+    qb = y + M * cd * 4
+    kb = qb + M * n_k * dk * 4
+    bd = kb + M * n_k * dk * 4
+    ob = bd + 2 * M * n_v * 4
+    cnt = ob + M * n_v * dv * 4 if M == 1 else 0
+    p2 = 1
+    while p2 < dk:
+        p2 <<= 1
+    if M == 1:
+        p = E.Program(asm, 'k_gdn_in1')
+        E.launch(p, mem, n_k, 256, p.pack_args([
+            dev['conv'], dev['cs'], qkv_d, dev['A'], dev['dt'], a_d, b_d, f32bits(eps), n_k, n_v, dk, dv, cd, y, qb, kb,
+            bd, cnt, bytes(40), 0, 0, 0]), dyn_lds=(2 * dk + p2 + p2 // 2) * 4)
+    else:
+        p = E.Program(asm, 'k_gdn_convEPKfS1_S1_iPf')
+        E.launch(p, mem, (M, (cd + 255) // 256), 256, p.pack_args([dev['conv'], dev['cs'], qkv_d, cd, y]))
+        p = E.Program(asm, 'k_gdn_conv_state')
+        E.launch(p, mem, (cd + 255) // 256, 256, p.pack_args([dev['cs'], qkv_d, M, cd]))
+        rows = M * n_k
+        p = E.Program(asm, f'k_gdn_prep_wILi{1 if dk <= 64 else 2}E')
+        E.launch(p, mem, (rows + 3) // 4, 256, p.pack_args([y, dev['A'], dev['dt'], a_d, b_d, f32bits(eps), rows, n_k, n_v,
+                                                            dk, cd, qb, kb, bd]))
+    R = dk if dk < 16 else 16
+    CW = 256 // R
+    rl = 2 * (2 * 32 * dk + 32 * CW + 2 * 32) * 4
+    tmpl = {4: (1, 4), 8: (1, 8), 16: (1, 16), 32: (2, 16), 64: (4, 16), 128: (8, 16)}[dk]
+    p = E.Program(asm, f'k_gdn_recILi{tmpl[0]}ELi{tmpl[1]}E')
+    E.launch(p, mem, (n_v, (dv + CW - 1) // CW), 256, p.pack_args([
+        dev['S'], qb, kb, y, bd, M, n_k, n_v, dv, cd, ob, dev['norm'], z_d, f32bits(eps), on_d, cnt]), dyn_lds=rl)
+    if M == 1:
+        return
+    rows = M * n_v
+    ept = 1 if dv <= 64 else 2 if dv <= 128 else 4
+    p = E.Program(asm, f'k_gdn_out_wILi{ept}E')
+    E.launch(p, mem, (rows + 3) // 4, 256, p.pack_args([ob, dev['norm'], z_d, f32bits(eps), rows, dv, on_d]))
+
+
+def test_gdn_prefill_decode_prefill(masm):
+    """dk = 128 (the 4B model's key dim, the same recurrence template) with 2 k heads over 4 v heads: a 6-token batch,
+    one decode token (conv, window update and prep in one launch; the gated norm run by the recurrence's last block),
+    then a 3-token batch; outputs, the conv window and the recurrent state against the oracle after each."""
+    import ctypes
+    n_k, n_v, dk, dv = 2, 4, 128, 32
+    rng = np.random.default_rng(4)
+    f32 = np.float32
+    cd = 2 * n_k * dk + n_v * dv
+    conv_w = (rng.standard_normal((cd, 4)) * 0.5).astype(f32)
+    A = (np.abs(rng.standard_normal(n_v)) + 0.1).astype(f32)
+    dt = (rng.standard_normal(n_v) * 0.5).astype(f32)
+    norm = (1 + 0.1 * rng.standard_normal(dv)).astype(f32)
+    mem = E.Memory()
+    dev = {n: mem.alloc(a.nbytes, a) for n, a in (('conv', conv_w), ('A', A), ('dt', dt), ('norm', norm))}
+    dev['cs'], dev['S'] = mem.alloc(3 * cd * 4), mem.alloc(n_v * dk * dv * 4)
+    cs, S = np.zeros((3, cd), f32), np.zeros((n_v, dk, dv), f32)
+    L = oracle.lib()
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    for M in (6, 1, 3):
+        qkv = rng.standard_normal((M, cd)).astype(f32)
+        z = rng.standard_normal((M, n_v, dv)).astype(f32)
+        a = rng.standard_normal((M, n_v)).astype(f32)
+        b = rng.standard_normal((M, n_v)).astype(f32)
+        qkv_d, z_d, a_d, b_d = (mem.alloc(x.nbytes, x) for x in (qkv, z, a, b))
+        on_d = mem.alloc(M * n_v * dv * 4)
+        emulate_gdn(masm['mixer.hip'], mem, dev, M, n_k, n_v, dk, dv, 1e-6, qkv_d, z_d, a_d, b_d, on_d)
+        on = np.zeros((M, n_v, dv), f32)
+        L.ora_gdn(ptr(conv_w), ptr(A), ptr(dt), ptr(norm), ptr(cs), ptr(S), ptr(qkv), ptr(z), ptr(a), ptr(b), f32(1e-6),
+                  M, n_k, n_v, dk, dv, ptr(on))
+        assert (mem.array(on_d, np.uint32, M * n_v * dv) == on.view(np.uint32).reshape(-1)).all(), f'on at M={M}'
+        assert (mem.array(dev['cs'], np.uint32, 3 * cd) == cs.view(np.uint32).reshape(-1)).all(), f'conv at M={M}'
+        assert (mem.array(dev['S'], np.uint32, n_v * dk * dv) == S.view(np.uint32).reshape(-1)).all(), f'S at M={M}'
