@@ -52,21 +52,28 @@ _LANE_MASKS = {}            # EXEC value -> per-lane bools (read-only, shared)
 
 # ------------------------------------------------------------------------------------------------ device memory
 class Memory:
-    """A flat device address space of numpy byte buffers."""
+    """The device address space: numpy byte buffers, each at its own host address (so addresses never collide, and
+    host code that copies into a buffer through its address -- the emulated runtime's memcpy -- is seen by the
+    kernels)."""
 
     def __init__(self):
         self.bufs = []              # (base, array)
-        self.next = 0x7F0000000000
 
     def alloc(self, nbytes, data=None):
-        arr = np.zeros(max(int(nbytes), 1), np.uint8)
+        """A zeroed buffer of nbytes at a 256-byte aligned address (filled from data when given)."""
+        n = max(int(nbytes), 1)
+        raw_arr = np.zeros(n + 256, np.uint8)
+        shift = (-raw_arr.ctypes.data) % 256
+        arr = raw_arr[shift:shift + n]
         if data is not None:
             raw = np.frombuffer(np.ascontiguousarray(data).tobytes(), np.uint8)
             arr[:raw.size] = raw
-        base = self.next
-        self.next += (arr.size + 0xFFFF) & ~0xFFFF
+        base = arr.ctypes.data
         self.bufs.append((base, arr))
         return base
+
+    def release(self, base):
+        self.bufs = [b for b in self.bufs if b[0] != base]
 
     def find(self, addr, n):
         for base, arr in self.bufs:
@@ -518,7 +525,12 @@ def round_fraction(f, dtype):
     d = float(f)                                  # correctly rounded to binary64
     if dtype == np.float64:
         return np.float64(d)
-    c = np.float32(d)
+    with np.errstate(over='ignore'):
+        c = np.float32(d)
+    if not np.isfinite(c):          # past the largest binary32: infinity from 2^128 - 2^103 (its midpoint) on
+        big = abs(f) >= Fraction(2 ** 128 - 2 ** 103)
+        m = np.float32(np.inf) if big else np.finfo(np.float32).max
+        return m if f > 0 else -m
     # correct a double rounding: pick the nearer binary32 neighbour of the exact value, ties to even
     lo = np.nextafter(c, np.float32(-np.inf)) if Fraction(float(c)) > f else c
     hi = np.nextafter(lo, np.float32(np.inf))
@@ -1519,97 +1531,114 @@ def _f32exp(x):
     return ((x.view(np.uint32) >> np.uint32(23)) & np.uint32(255)).astype(np.int64)
 
 
-@op('v_div_scale_f32')
-def _(w, i):
-    """Pre-scaling of the correctly rounded division sequence (S0 the value to scale, S1 the denominator, S2 the
-    numerator).  Zero operands give NaN (the final fixup then produces the signed infinity or NaN); the operand
-    ranges that need scaling (denormals, quotients near the overflow or underflow range, tiny numerators) are not
-    modelled and raise."""
-    s0, s1, s2 = (w.fsrc(i.ops[k]) for k in (2, 3, 4))
-    act = w.lanes()
-    zero = (s1 == 0) | (s2 == 0)
+# The correctly rounded division sequence the compiler emits: v_div_scale (twice: the denominator and the
+# numerator), a reciprocal and Newton steps, v_div_fmas, v_div_fixup.  Semantics from the instruction set reference's
+# pseudocode; per type: (bias, exponent gap near overflow, scale exponent, tiny-numerator exponent bound, underflow gap,
+# top exponent).
+_DIV = {np.float32: (127, 96, 64, 23, -150, 255), np.float64: (1023, 768, 128, 53, -1075, 2047)}
+
+
+def _fexp(x, dt):
+    return _f32exp(x) if dt == np.float32 else _f64exp(x)
+
+
+def _is_denorm(x, dt):
+    return (_fexp(x, dt) == 0) & (x != 0)
+
+
+def _div_scale(w, i, dt):
+    """D = S0 (the value to scale: S1 the denominator or S2 the numerator) scaled by 2^+-s so that the reciprocal and
+    the Newton steps stay in range; VCC marks the lanes whose quotient comes out scaled (undone by v_div_fmas).
+    In priority order: a zero operand gives NaN; a quotient near overflow (exponent gap >= the type's bound) scales
+    the denominator up and sets VCC; a denormal denominator scales both up; 1/S1 denormal (in binary64) with a
+    denormal quotient scales the denominator up and sets VCC; 1/S1 denormal alone scales both down; a denormal
+    quotient scales the numerator up and sets VCC; a tiny numerator scales both up."""
+    bias, gap, sc, tiny, _, _ = _DIV[dt]
+    s0, s1, s2 = (w.fsrc(i.ops[k], dt) for k in (2, 3, 4))
+    e1, e2 = _fexp(s1, dt), _fexp(s2, dt)
     with np.errstate(all='ignore'):
-        e1, e2 = _f32exp(s1), _f32exp(s2)
-        edge = ~zero & ((e2 - e1 >= 96) | (e1 == 0) | (e2 <= 23) | (np.abs(np.float32(1) / s1) < np.float32(2 ** -126))
-                        | (np.abs(s2 / s1) < np.float32(2 ** -126)) | ~np.isfinite(s1) | ~np.isfinite(s2))
-    if (edge & act).any():
-        raise EmuError('v_div_scale_f32 on operands that need scaling: not modelled')
-    out = np.where(zero, np.float32(np.nan), s0).astype(np.float32)
-    w.vset(i.ops[0], out.view(np.uint32))
-    set_mask(w, i.ops[1], np.zeros(64, bool))
+        r64 = np.float64(1.0) / s1.astype(np.float64)
+        rcp_den = _is_denorm(r64, np.float64)
+        quo_den = _is_denorm((s2 / s1).astype(dt), dt)
+        up, down = np.ldexp(s0, sc).astype(dt), np.ldexp(s0, -sc).astype(dt)
+    out = s0.copy()
+    vcc = np.zeros(64, bool)
+    undecided = np.ones(64, bool)
+
+    def case(cond, value=None, set_vcc=False):
+        nonlocal out, vcc, undecided
+        c = undecided & cond
+        if value is not None:
+            out = np.where(c, value, out)
+        if set_vcc:
+            vcc = vcc | c
+        undecided = undecided & ~c
+    case((s1 == 0) | (s2 == 0), dt(np.nan))
+    case(e2 - e1 >= gap, np.where(s0 == s1, up, s0), True)
+    case(_is_denorm(s1, dt), up)
+    case(rcp_den & quo_den, np.where(s0 == s1, up, s0), True)
+    case(rcp_den, down)
+    case(quo_den, np.where(s0 == s2, up, s0), True)
+    case(e2 <= tiny, up)
+    w.vset(i.ops[0], out.astype(dt).view(np.uint32 if dt == np.float32 else np.uint64), 1 if dt == np.float32 else 2)
+    set_mask(w, i.ops[1], vcc)
 
 
-@op('v_div_fmas_f32')
-def _(w, i):
-    vcc = (np.uint64(w.s[106] | (w.s[107] << 32)) >> LANES.astype(np.uint64)) & np.uint64(1)
-    if (vcc.astype(bool) & w.lanes()).any():
-        raise EmuError('v_div_fmas_f32 with VCC set (scaled division): not modelled')
-    a, b, c = (w.fsrc(i.ops[k]) for k in (1, 2, 3))
-    w.vset(i.ops[0], exact_fma(a, b, c, np.float32).view(np.uint32))
-
-
-def _div_fixup(w, i, dt):
-    """Special cases of the division sequence's final step (the instruction set reference's table): NaN operands,
-    0/0 and inf/inf give the default NaN; x/0 and inf/y a signed infinity; x/inf and 0/y a signed zero; otherwise
-    the quotient with the sign of num/den.  Quotients that would underflow or overflow raise (not modelled)."""
-    q, den, num = (w.fsrc(i.ops[k], dt) for k in (1, 2, 3))
-    sign = np.signbit(den) ^ np.signbit(num)
-    out = np.where(sign, -np.abs(q), np.abs(q)).astype(dt)
-    qnan = np.array([0xFFC00000], np.uint32).view(np.float32)[0] if dt == np.float32 else \
-        np.array([0xFFF8000000000000], np.uint64).view(np.float64)[0]
-    nan = np.isnan(num) | np.isnan(den)
-    zz = (den == 0) & (num == 0)
-    ii = np.isinf(den) & np.isinf(num)
-    xinf = ((den == 0) | np.isinf(num)) & ~zz & ~ii & ~nan
-    xzero = (np.isinf(den) | (num == 0)) & ~xinf & ~zz & ~ii & ~nan
-    out = np.where(xzero, np.where(sign, dt(-0.0), dt(0.0)), out)
-    out = np.where(xinf, np.where(sign, dt(-np.inf), dt(np.inf)), out)
-    out = np.where(zz | ii, qnan, out)
-    out = np.where(np.isnan(num), num, np.where(np.isnan(den), den, out))
-    ordinary = ~(nan | (den == 0) | (num == 0) | np.isinf(den) | np.isinf(num))
-    ex = _f32exp if dt == np.float32 else _f64exp
-    lo, top = (-150, 255) if dt == np.float32 else (-1075, 2047)
-    with np.errstate(all='ignore'):
-        edge = ordinary & ((ex(num) - ex(den) < lo) | (ex(den) == top))
-    if (edge & w.lanes()).any():
-        raise EmuError('division fixup near the underflow or overflow range: not modelled')
+def _div_fmas(w, i, dt):
+    """fma(S0, S1, S2), on VCC lanes scaled by 2^+s when S2 (the scaled quotient) has exponent >= the bias, else
+    2^-s, with one rounding of the exact scaled value."""
+    bias, _, sc, _, _, _ = _DIV[dt]
+    a, b, c = (w.fsrc(i.ops[k], dt) for k in (1, 2, 3))
+    out = exact_fma(a, b, c, dt)
+    vcc = ((np.uint64(w.s[106] | (w.s[107] << 32)) >> LANES.astype(np.uint64)) & np.uint64(1)).astype(bool)
+    for l in np.nonzero(vcc & w.lanes())[0]:
+        x, y, z = float(a[l]), float(b[l]), float(c[l])
+        if not all(np.isfinite(v) for v in (x, y, z)):
+            with np.errstate(all='ignore'):
+                out[l] = dt(x * y + z) * dt(2.0 ** (sc if _fexp(c[l:l + 1], dt)[0] >= bias else -sc))
+            continue
+        e = sc if _fexp(c[l:l + 1], dt)[0] >= bias else -sc
+        out[l] = round_fraction((Fraction(x) * Fraction(y) + Fraction(z)) * Fraction(2) ** e, dt)
     w.vset(i.ops[0], out.astype(dt).view(np.uint32 if dt == np.float32 else np.uint64), 1 if dt == np.float32 else 2)
 
 
-@op('v_div_fixup_f32')
-def _(w, i): _div_fixup(w, i, np.float32)
+def _div_fixup(w, i, dt):
+    """The sequence's final step (S0 the quotient, S1 the denominator, S2 the numerator): a NaN operand is returned
+    quieted; 0/0 and inf/inf give the default NaN; x/0 and inf/y a signed infinity; x/inf and 0/y a signed zero; an
+    exponent gap below the type's underflow bound a signed zero, a denominator with the top exponent a signed
+    infinity; otherwise |S0| with the sign of num/den."""
+    _, _, _, _, lo, top = _DIV[dt]
+    q, den, num = (w.fsrc(i.ops[k], dt) for k in (1, 2, 3))
+    ut = np.uint32 if dt == np.float32 else np.uint64
+    quiet = ut(1 << 22) if dt == np.float32 else ut(1 << 51)
+    sign = np.signbit(den) ^ np.signbit(num)
+    signed = lambda v: np.where(sign, dt(-v), dt(v)).astype(dt)
+    out = np.where(sign, -np.abs(q), np.abs(q)).astype(dt)
+    qnan = np.array([0xFFC00000], np.uint32).view(np.float32)[0] if dt == np.float32 else \
+        np.array([0xFFF8000000000000], np.uint64).view(np.float64)[0]
+    conds = [
+        (np.isnan(num), (num.view(ut) | quiet).view(dt)),
+        (np.isnan(den), (den.view(ut) | quiet).view(dt)),
+        ((den == 0) & (num == 0), np.full(64, qnan, dt)),
+        (np.isinf(den) & np.isinf(num), np.full(64, qnan, dt)),
+        ((den == 0) | np.isinf(num), signed(np.inf)),
+        (np.isinf(den) | (num == 0), signed(0.0)),
+        (_fexp(num, dt) - _fexp(den, dt) < lo, signed(0.0)),
+        (_fexp(den, dt) == top, signed(np.inf)),
+    ]
+    for cond, val in reversed(conds):
+        out = np.where(cond, val, out)
+    w.vset(i.ops[0], out.astype(dt).view(ut), 1 if dt == np.float32 else 2)
 
 
 def _f64exp(x):
     return ((x.view(np.uint64) >> np.uint64(52)) & np.uint64(0x7FF)).astype(np.int64)
 
 
-@op('v_div_scale_f64')
-def _(w, i):
-    s0, s1, s2 = (w.fsrc(i.ops[k], np.float64) for k in (2, 3, 4))
-    act = w.lanes()
-    zero = (s1 == 0) | (s2 == 0)
-    with np.errstate(all='ignore'):
-        e1, e2 = _f64exp(s1), _f64exp(s2)
-        edge = ~zero & ((e2 - e1 >= 768) | (e1 == 0) | (e2 <= 53) | (np.abs(1.0 / s1) < 2.0 ** -1022)
-                        | (np.abs(s2 / s1) < 2.0 ** -1022) | ~np.isfinite(s1) | ~np.isfinite(s2))
-    if (edge & act).any():
-        raise EmuError('v_div_scale_f64 on operands that need scaling: not modelled')
-    w.vset(i.ops[0], np.where(zero, np.nan, s0).view(np.uint64), 2)
-    set_mask(w, i.ops[1], np.zeros(64, bool))
-
-
-@op('v_div_fmas_f64')
-def _(w, i):
-    vcc = (np.uint64(w.s[106] | (w.s[107] << 32)) >> LANES.astype(np.uint64)) & np.uint64(1)
-    if (vcc.astype(bool) & w.lanes()).any():
-        raise EmuError('v_div_fmas_f64 with VCC set (scaled division): not modelled')
-    a, b, c = (w.fsrc(i.ops[k], np.float64) for k in (1, 2, 3))
-    w.vset(i.ops[0], exact_fma(a, b, c, np.float64).view(np.uint64), 2)
-
-
-@op('v_div_fixup_f64')
-def _(w, i): _div_fixup(w, i, np.float64)
+for _t, _dt in (('f32', np.float32), ('f64', np.float64)):
+    H[f'v_div_scale_{_t}'] = (lambda dt: lambda w, i: _div_scale(w, i, dt))(_dt)
+    H[f'v_div_fmas_{_t}'] = (lambda dt: lambda w, i: _div_fmas(w, i, dt))(_dt)
+    H[f'v_div_fixup_{_t}'] = (lambda dt: lambda w, i: _div_fixup(w, i, dt))(_dt)
 
 
 # --- matrix core
@@ -1997,15 +2026,16 @@ def _scratch_off(w, i, vaddr, saddr):
 
 # ------------------------------------------------------------------------------------------------ workgroups
 class Workgroup:
-    def __init__(self, prog, mem, wg_id, nthreads, wg_id_y=0, dyn_lds=0, wg_id_z=0):
+    def __init__(self, prog, mem, wg_id, nthreads, wg_id_y=0, dyn_lds=0, wg_id_z=0, kernarg=0):
         self.prog, self.mem = prog, mem
+        self.wg_ids = (wg_id, wg_id_y, wg_id_z)
         self.lds_size = prog.lds_bytes + dyn_lds
         self.lds = np.zeros(max(self.lds_size, 4) + 16, np.uint8)
         self.lds_busy = np.zeros(self.lds.size, np.int32)     # bytes that pending copies will write
         self.waves = []
         for wv in range((nthreads + 63) // 64):
             w = Wave(self, wv, prog)
-            w.s[0], w.s[1] = KERNARG & MASK32, KERNARG >> 32
+            w.s[0], w.s[1] = kernarg & MASK32, kernarg >> 32
             w.s[2] = wg_id
             k = 3
             if prog.wg_id_y:
@@ -2077,7 +2107,7 @@ class Workgroup:
                     except EmuError as e:
                         if ' pc ' in str(e):
                             raise
-                        raise EmuError(f'workgroup {w.s[2]} wave {w.wid} pc {w.pc} ({ins.text}): {e}') from None
+                        raise EmuError(f'workgroup {self.wg_ids} wave {w.wid} pc {w.pc} ({ins.text}): {e}') from None
                     except Exception as e:
                         raise EmuError(f'wave {w.wid} pc {w.pc} ({ins.text}): {type(e).__name__}: {e}') from e
                     if TRACE is not None:
@@ -2111,7 +2141,6 @@ def indexed(ins, idx, which):
     return new
 
 
-KERNARG = 0x7E0000000000
 TRACE = None          # debugging hook: called with (wave, instruction) after each instruction
 
 
@@ -2126,7 +2155,8 @@ def launch(prog, mem, grid, block, kernarg_bytes, dyn_lds=0):
     """Runs every workgroup of the grid (an int, or (x, y) for a 2-D grid) in order, x fastest."""
     if len(kernarg_bytes) > prog.kernarg_size:
         raise EmuError('kernel arguments larger than the kernel expects')
-    ka = np.zeros(max(prog.kernarg_size, 8) + 64, np.uint8)
+    kbase = mem.alloc(max(prog.kernarg_size, 8) + 64)
+    ka = mem.array(kbase, np.uint8, max(prog.kernarg_size, 8) + 64)
     ka[:len(kernarg_bytes)] = np.frombuffer(bytes(kernarg_bytes), np.uint8)
     gx, gy, gz = (grid, 1, 1) if isinstance(grid, int) else (tuple(grid) + (1, 1))[:3]
     if (gy > 1 and not prog.wg_id_y) or (gz > 1 and not prog.wg_id_z):
@@ -2140,11 +2170,12 @@ def launch(prog, mem, grid, block, kernarg_bytes, dyn_lds=0):
         if kind == 'hidden_dynamic_lds_size':
             v = dyn_lds
         ka[off:off + size] = np.frombuffer(int(v).to_bytes(size, 'little'), np.uint8)
-    mem.bufs = [b for b in mem.bufs if b[0] != KERNARG]
-    mem.bufs.append((KERNARG, ka))
     steps = 0
-    for z in range(gz):
-        for y in range(gy):
-            for x in range(gx):
-                steps += Workgroup(prog, mem, x, block, y, dyn_lds, z).run()
+    try:
+        for z in range(gz):
+            for y in range(gy):
+                for x in range(gx):
+                    steps += Workgroup(prog, mem, x, block, y, dyn_lds, z, kernarg=kbase).run()
+    finally:
+        mem.release(kbase)
     return steps
