@@ -23,6 +23,8 @@ emu_release_fn g_release = nullptr;
 int g_cus = 256;
 hipError_t g_error = hipSuccess;
 std::map<const void*, std::string> g_kernels;          // host stub -> device symbol
+struct Var { size_t size; void* dev; };
+std::map<const void*, Var> g_vars;                     // host shadow of a __device__ variable -> its device copy
 struct Config { dim3 grid, block; size_t shared; hipStream_t stream; };
 std::vector<Config> g_configs;
 void* g_fatbin_handle = nullptr;
@@ -42,6 +44,16 @@ void __hipUnregisterFatBinary(void**) {}
 void __hipRegisterFunction(void**, const void* host_function, char*, const char* device_name, unsigned int, uint3*,
                            uint3*, dim3*, dim3*, int*) {
     g_kernels[host_function] = device_name;
+}
+
+// __device__ variables: the size at registration; device memory (zeroed) on the first hipGetSymbolAddress
+void __hipRegisterVar(void**, void* var, char*, char*, int, size_t size, int, int) { g_vars[var] = {size, nullptr}; }
+hipError_t hipGetSymbolAddress(void** p, const void* symbol) {
+    const auto it = g_vars.find(symbol);
+    if (it == g_vars.end() || !g_alloc) return g_error = hipErrorInvalidSymbol;
+    if (!it->second.dev) it->second.dev = g_alloc(it->second.size);
+    *p = it->second.dev;
+    return *p ? hipSuccess : (g_error = hipErrorOutOfMemory);
 }
 
 hipError_t __hipPushCallConfiguration(dim3 grid, dim3 block, size_t shared, hipStream_t stream) {
