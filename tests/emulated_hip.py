@@ -144,6 +144,8 @@ def pytest_configure(config):
 def pytest_unconfigure(config):
     """With DET_EMU_LOG set: the device symbols launched in this session, one per line, into that file."""
     path = os.environ.get('DET_EMU_LOG')
+    if path and os.environ.get('PYTEST_XDIST_WORKER'):
+        path += '.' + os.environ['PYTEST_XDIST_WORKER']     # one file per worker process
     if path and _INSTALLED is not None:
         with open(path, 'w') as fh:
             fh.write('\n'.join(_INSTALLED.kernels_run()) + '\n')

@@ -54,14 +54,20 @@ def emu_env(tmp_path_factory):
     return env
 
 
-def run_selected(env, ids, log):
+def run_selected(env, ids, log, workers=1):
+    """The ids in one pytest run under the stand-in (workers > 1: that many processes, each with its own stand-in
+    and emulator); returns the device symbols launched."""
     env = dict(env, DET_EMU_LOG=str(log))
+    par = ['-n', str(workers)] if workers > 1 else []
     r = subprocess.run([sys.executable, '-m', 'pytest', '-p', 'tests.emulated_hip', '-m', 'gpu', '-q', '-x',
-                        '-p', 'no:cacheprovider', *ids], cwd=ROOT, env=env, capture_output=True, text=True,
+                        '-p', 'no:cacheprovider', *par, *ids], cwd=ROOT, env=env, capture_output=True, text=True,
                        timeout=1500)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-4000:]
     assert ' passed' in r.stdout and 'skipped' not in r.stdout, r.stdout[-2000:]
-    return open(log).read().split()
+    names = set()
+    for p in log.parent.glob(log.name + '*'):
+        names.update(p.read_text().split())
+    return sorted(names)
 
 
 def launched(names, part):
@@ -69,7 +75,7 @@ def launched(names, part):
 
 
 def test_gpu_tests_through_the_library(emu_env, tmp_path):
-    names = run_selected(emu_env, SELECTED, tmp_path / 'kernels')
+    names = run_selected(emu_env, SELECTED, tmp_path / 'kernels', workers=4)
     for k in ('k_decodeILi', 'k_decode_ms', 'k_prefill2', 'k_repackE', 'k_repack_pf', 'k_qrow', 'k_quantize',
               'k_attn', 'k_gdn', 'k_argmax'):
         assert launched(names, k), (k, names)
