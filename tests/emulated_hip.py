@@ -20,8 +20,6 @@ import subprocess
 import sys
 import traceback
 
-import numpy as np
-
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SHIM_SRC = os.path.join(ROOT, 'tests', 'emu_runtime', 'hip_on_emulator.cpp')
 SHIM_MAP = os.path.join(ROOT, 'tests', 'emu_runtime', 'versions.map')
