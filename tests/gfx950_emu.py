@@ -1484,7 +1484,9 @@ def _(w, i): w.vset(i.ops[0], w.vget(i.ops[1]).astype(np.float64).view(np.uint64
 
 
 @op('v_cvt_f32_f64')
-def _(w, i): w.vset(i.ops[0], w.fsrc(i.ops[1], np.float64).astype(np.float32).view(np.uint32))
+def _(w, i):
+    with np.errstate(over='ignore'):        # beyond the binary32 range: infinity, as round to nearest gives
+        w.vset(i.ops[0], w.fsrc(i.ops[1], np.float64).astype(np.float32).view(np.uint32))
 
 
 @op('v_rndne_f32')
