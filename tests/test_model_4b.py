@@ -40,6 +40,7 @@ def log(msg, t0=[time.time()]):
         f.write(line + '\n')
 
 
+@pytest.mark.long
 @pytest.mark.timeout(1500)
 def test_qwen35_4b_prefill_512_and_greedy_decode(tmp_path):
     cfg = dict(bench.QWEN35_4B)
