@@ -750,8 +750,9 @@ void det_linear_sizes(int N, int K, int bits, size_t* wq_bytes, size_t* c_bytes,
     if (bits != 4 && bits != 6 && bits != 8) DET_FAIL("det_linear_sizes: unsupported bits=%d", bits);
     // whole 128-row blocks (pairs of 64-row tiles): the prefill kernel reads weight tiles two at a time
     const size_t T = 2 * (((size_t)N + 2 * TILE_N - 1) / (2 * TILE_N)), G = (size_t)K / GROUP;
-    // the decode tiles, then the prefill planes (the same size: 32-row blocks of the same row pairs)
-    if (wq_bytes) *wq_bytes = 2 * T * G * group_bytes(bits) * TILE_N;
+    // the decode tiles, then (only when the stream-K prefill kernel is selected) the prefill planes: the same size,
+    // 32-row blocks of the same row pairs
+    if (wq_bytes) *wq_bytes = (use_streamk() ? 2 : 1) * T * G * group_bytes(bits) * TILE_N;
     if (c_bytes) *c_bytes = T * TILE_N * 4;
     if (m_bytes) *m_bytes = T * G * TILE_N * 2;
 }
@@ -764,7 +765,7 @@ void det_linear_repack(const uint8_t* rows, int N, int K, int bits, uint8_t* wq,
     const size_t blocks = std::min<size_t>((nchunks + 255) / 256, 65536);
     k_repack<<<(unsigned)blocks, 256, 0, st>>>(rows, N, K, bits, wq, c, m, nchunks);
     DET_CHECK(hipGetLastError());
-    prefill_repack(rows, N, K, bits, wq, st);
+    if (use_streamk()) prefill_repack(rows, N, K, bits, wq, st);
 }
 
 void det_quantize_rows(const float* w, int N, int K, int bits, uint8_t* rows, hipStream_t st) {

@@ -192,6 +192,7 @@ __device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
 
 // prefill.hip: the prefill planes inside a linear's wq buffer, their load-time repack, and the GEMM for M > 64
 // (returns false, having launched nothing, when the shape is outside what the kernel covers)
+__attribute__((visibility("hidden"))) bool use_streamk();
 __attribute__((visibility("hidden"))) size_t pf_offset(int N, int K, int bits);
 __attribute__((visibility("hidden"))) void prefill_repack(const uint8_t* rows, int N, int K, int bits, uint8_t* wq, hipStream_t st);
 __attribute__((visibility("hidden"))) bool prefill_gemm(const det_qlinear& L, const int8_t* xq, const float* sx,

@@ -861,8 +861,12 @@ void launch_prefill2(const det_qlinear& L, const int8_t* xq, const float* sx, co
     DET_CHECK(hipGetLastError());
 }
 
+} // namespace
+
 // Which kernel serves M > 64: the 128 x 64-tile kernel k_prefill2, or the stream-K kernel k_prefill when the
-// environment sets DET_PREFILL=streamk (read once).
+// environment sets DET_PREFILL=streamk (read once, so that a linear's layout and the kernel that reads it agree for
+// the life of the process).  Only the stream-K kernel reads the prefill planes: without it they are neither
+// reserved nor written.
 bool use_streamk() {
     static const int v = [] {
         const char* e = getenv("DET_PREFILL");
@@ -870,8 +874,6 @@ bool use_streamk() {
     }();
     return v != 0;
 }
-
-} // namespace
 
 // byte offset of the prefill planes inside a linear's wq buffer (after the decode tiles)
 size_t pf_offset(int N, int K, int bits) {

@@ -254,10 +254,14 @@ def test_repack_writes_in_bounds(N, K, bits):
     from det_amd import ffi
     if not os.path.exists(ffi.LIB_PATH):
         pytest.skip('libdet_hip.so not built')
-    wq_bytes, c_bytes, m_bytes = ffi.linear_sizes(N, K, bits)
+    wq_dec, c_bytes, m_bytes = ffi.linear_sizes(N, K, bits)
     G = K // GROUP
     T = 2 * ((N + 127) // 128)                              # 64-row tiles, whole pairs
     pf_offset = T * G * GB[bits] * 64                       # prefill.hip pf_offset
+    # without DET_PREFILL=streamk (this process) wq holds the decode tiles only; with it, the prefill planes follow
+    # and wq is twice as large (test_linear_sizes_with_streamk checks that size in a child process)
+    assert wq_dec == pf_offset
+    wq_bytes = 2 * pf_offset
     rb = K // 32 * BPL[bits] + 4 + 2 * G
     # k_repack: idx < nchunks = pf_offset / 16; lane r = idx % 64, chunk c, group g, tile
     nchunks = pf_offset // 16                               # (wq_bytes / 16 would overrun m and c)
@@ -278,3 +282,25 @@ def test_repack_writes_in_bounds(N, K, bits):
     assert hi == wq_bytes, (hi, wq_bytes)
     # both kernels together write every byte of wq exactly once: the regions abut and have the sizes written above
     assert nchunks * 16 + items // 64 * NP[bits] * 1024 == wq_bytes
+
+
+def test_linear_sizes_with_streamk():
+    """det_linear_sizes reserves the prefill planes (doubling wq) only when DET_PREFILL=streamk selects the kernel that
+    reads them; c and m are the same either way."""
+    import os
+    import subprocess
+    import sys
+    from det_amd import ffi
+    if not os.path.exists(ffi.LIB_PATH):
+        pytest.skip('libdet_hip.so not built')
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ('import sys; sys.path.insert(0, %r); from det_amd import ffi; '
+            'print(*ffi.linear_sizes(9728, 2560, 6))' % root)
+    got = {}
+    for mode in ('', 'streamk'):
+        env = dict(os.environ, DET_PREFILL=mode)
+        out = subprocess.run([sys.executable, '-c', code], env=env, capture_output=True, text=True, check=True)
+        got[mode] = [int(v) for v in out.stdout.split()]
+    dec, sk = got[''], got['streamk']
+    assert sk[0] == 2 * dec[0] and sk[1:] == dec[1:]
+    assert dec[0] == 152 * 20 * 96 * 64                     # 152 tiles of 64 rows (76 pairs), 20 groups, 96 B each
