@@ -620,7 +620,10 @@ size_t g_user_scratch_bytes = 0;
 
 // K-split buffers of k_decode: int64 accumulators part[MP][Npad] and per-tile arrival counters, zero between calls
 // (the last workgroup of each tile clears what it used); library-owned, grown on demand.  Calls that overlap on
-// different streams would share them: det runs every call on one in-order stream.
+// different streams would share them: det runs every call on one in-order stream.  The zero-between-calls invariant
+// holds only while every launch completes: a kernel that faults part-way leaves counts behind, which is why such a
+// fault is fatal (det_sync and DET_CHECK abort) rather than something a caller recovers from and calls again.
+// These buffers are the library's own and are not counted by det_allocated_bytes.
 long long* g_part = nullptr;
 size_t g_part_cap = 0;              // elements
 unsigned int* g_cnt = nullptr;

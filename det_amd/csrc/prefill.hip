@@ -802,8 +802,9 @@ __global__ void __launch_bounds__(256, 3) k_prefill2(const uint8_t* __restrict__
     }
 }
 
-// library-owned stream-K buffers: partial tiles (two slots per workgroup) and per-tile arrival counters, the
-// counters zero between calls (the finishing workgroup resets its tile's)
+// library-owned stream-K / K-slice buffers: partial tiles and per-tile arrival counters, the counters zero between
+// calls (the finishing workgroup resets its tile's; a launch that fails part-way breaks this, and the library treats
+// every kernel fault as fatal).  Not counted by det_allocated_bytes.
 long long* g_pf_part = nullptr;
 size_t g_pf_part_cap = 0;
 unsigned int* g_pf_cnt = nullptr;

@@ -7,6 +7,7 @@
 //   * det_sync waits for the device and aborts when a kernel failed;
 //   * every operation runs on the null stream, det's one in-order stream.
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
@@ -73,11 +74,13 @@ private:
     size_t live_ = 0;
 };
 
-bool g_touched = false;     // set once the device state exists: det_free and det_allocated_bytes never create it
+// set once the device state exists: det_free and det_allocated_bytes never create it.  Atomic: any thread may be
+// the first to call device() while another reads the flag.
+std::atomic<bool> g_touched{false};
 
 DeviceState& device() {
     DeviceState& d = DeviceState::instance();
-    g_touched = true;
+    g_touched.store(true, std::memory_order_release);
     return d;
 }
 
@@ -197,7 +200,7 @@ void* det_hip_stream(void) { device(); return nullptr; }          // the null st
 void* det_malloc(size_t bytes) { return device().allocate(bytes); }
 
 void det_free(void* p) {
-    if (!p || !g_touched) return;            // nothing was ever allocated: nothing to release
+    if (!p || !g_touched.load(std::memory_order_acquire)) return;     // nothing was ever allocated: nothing to release
     if (!device().forget(p)) {
         fprintf(stderr, "det_free: %p was not returned by det_malloc (or was freed already)\n", p);
         abort();
@@ -206,7 +209,7 @@ void det_free(void* p) {
     DET_CHECK(hipFree(p));
 }
 
-size_t det_allocated_bytes(void) { return g_touched ? device().live() : 0; }
+size_t det_allocated_bytes(void) { return g_touched.load(std::memory_order_acquire) ? device().live() : 0; }
 
 void det_sync(void) {
     device();

@@ -21,7 +21,7 @@ int         det_init(void);                 // selects the current device; 0 on 
 const char* det_device_name(void);
 void*       det_malloc(size_t bytes);       // a device block filled with zero bytes, or NULL when none is available
 void        det_free(void* p);              // waits for pending work first; aborts on a pointer det_malloc did not return
-size_t      det_allocated_bytes(void);
+size_t      det_allocated_bytes(void);      // live det_malloc bytes (the GEMM's own partial-sum buffers not included)
 void        det_sync(void);                 // returns once the device is idle; a failed kernel ends the process
 void        det_flush(void);                // nothing to do: every launch reaches the device when it is made
 void        det_memset(void* p, int value, size_t bytes, hipStream_t st);
@@ -34,7 +34,8 @@ void*       det_hip_stream(void);           // the stream det's work runs on (de
 //   wq: packed codes in 64-row tiles, [T][K/128][GB/16][64 rows][16 bytes] with T = 2*ceil(N/128) (whole pairs of
 //       tiles), where GB = 128, 96, 64 bytes is one row's packed 128-group (4 * bytes_per_32) for W8, W6, W4; the
 //       16-byte chunk c of a tile row is bytes [16c, 16c+16) of that row's packed group, exactly as in the det row;
-//       rows past N are zero.  The same number of bytes follows: the prefill planes, per 32-row block and 128-group
+//       rows past N are zero.  Only when the environment sets DET_PREFILL=streamk (read once per process), the same
+//       number of bytes follows: the prefill planes, per 32-row block and 128-group
 //       one 16-byte word per lane and plane (4, 3, 2 planes for W8, W6, W4), holding the codes of one row and
 //       k-half in the order and scaled packing the M > 64 kernel feeds to the matrix core;
 //   c:  [T*64] fp32 (zero past N);

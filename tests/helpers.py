@@ -118,3 +118,27 @@ def det_rows_from(codes, c, m, bits):
     packed = spec_np.pack_codes(np.asarray(codes, np.int8), bits)
     return np.concatenate([packed, np.asarray(c, np.float32).reshape(N, 1).view(np.uint8),
                            np.asarray(m, '<u2').view(np.uint8)], axis=1)
+
+
+# Groups of K = 128 for which two of the quantizer's 11 candidate scales give the same least squared error, in exact
+# rational arithmetic and in the binary64 sequential sum alike (quantize.rs:50-52: strict <, the first candidate
+# wins).  The group's amax is qmax * 5, so base = 5 and the candidates are 5 * (0.80 + 0.02 step); the listed values
+# are half-integers and the rest of the group is zero.  W4: steps 5 (s = 4.5) and 10 (s = 5) both give 80.
+# W6: steps 9 (s = 4.9) and 10 (s = 5) both give 104.5.  Found by a seeded random search over half-integer groups.
+TIE_GROUPS = {
+    4: ((5, 10), [35.0, 17.0, 10.5, -20.5, -30.5, -8.5, 9.5, -22.0, -25.5, 24.5, 21.5, -19.5, 16.0, -31.5, -24.5,
+                  -30.5, 8.0, 17.5, -13.5, 30.0, 5.5, -17.0, 26.0, -23.0, 1.5, 7.5, 23.0, 6.5, -21.0, -12.0, 26.0,
+                  -24.0, 14.0, 23.5, -3.0, -8.5, -31.5, -34.5, 7.0, 4.5, 26.5]),
+    6: ((9, 10), [155.0, -83.0, -53.0, -128.5, -148.5, 4.5, 76.5, -146.5, 80.5, 109.0, 30.5, -9.5, -53.0, -10.0,
+                  93.5, -60.0, 91.0, 73.0, -27.5, 35.5, 76.5, 141.5, -99.5, -62.0, -141.0, -80.5, 64.0, 96.5, 7.5,
+                  -23.5, 109.5, -14.0, 30.5, 25.5, -7.0, 131.5, -141.0, 126.0, 141.0, 83.5, 67.5, -135.5, -67.5,
+                  -85.0, 85.5, 144.0, -107.5, 4.5, 8.5, -144.0, -113.5, 51.0, -20.0, -88.5, 53.5, 39.5, 136.0]),
+}
+
+
+def tie_group(bits, scale=1.0):
+    """The tie group of TIE_GROUPS[bits] as a float32[128], times `scale` (a power of two keeps the tie)."""
+    w = np.zeros(128, np.float32)
+    vals = TIE_GROUPS[bits][1]
+    w[:len(vals)] = np.asarray(vals, np.float32) * np.float32(scale)
+    return w

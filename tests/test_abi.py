@@ -36,8 +36,9 @@ def test_linear_sizes(N, K, bits):
     wq, c, m = ffi.linear_sizes(N, K, bits)
     T = 2 * ((N + 127) // 128)                         # whole pairs of 64-row tiles
     G = K // 128
-    # the decode tiles and then the prefill planes, each T * G * 64 rows' packed groups
-    assert wq == 2 * T * G * 64 * 4 * {8: 32, 6: 24, 4: 16}[bits]
+    # the decode tiles: T * G * 64 rows' packed groups (the prefill planes of the same size follow them only under
+    # DET_PREFILL=streamk, checked by test_prefill_logic.py::test_linear_sizes_with_streamk)
+    assert wq == T * G * 64 * 4 * {8: 32, 6: 24, 4: 16}[bits]
     assert c == T * 64 * 4
     assert m == T * G * 64 * 2
 

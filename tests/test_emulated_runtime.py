@@ -30,6 +30,8 @@ SELECTED = [
     'tests/test_quant_parity.py::test_conformance_norms',
     'tests/test_quant_parity.py::test_scale_underflow_rows',
     'tests/test_quantizer_parity.py::test_quantizer_bytes[37-128-6]',
+    'tests/test_quantizer_parity.py::test_quantizer_tie_takes_the_first[4]',
+    'tests/test_quantizer_parity.py::test_repack_layout[6]',
     'tests/test_mixer_parity.py::test_argmax_first_of_ties',
     'tests/test_mixer_parity.py::test_argmax_nan_and_signed_zero',
     'tests/test_mixer_parity.py::test_gdn_small_shapes[1-2-4-4]',
@@ -38,7 +40,8 @@ SELECTED = [
     'tests/test_gemm_parity.py::test_conformance_fused_parts',
     'tests/test_gemm_parity.py::test_four_parts_and_accumulate_edges[6]',
 ]
-STREAMK = ['tests/test_gemm_parity.py::test_four_parts_and_accumulate_edges[4]']
+STREAMK = ['tests/test_gemm_parity.py::test_four_parts_and_accumulate_edges[4]',
+           'tests/test_quantizer_parity.py::test_prefill_planes[8]']
 
 
 @pytest.fixture(scope='module')
@@ -58,6 +61,10 @@ def run_selected(env, ids, log, workers=1):
     """The ids in one pytest run under the stand-in (workers > 1: that many processes, each with its own stand-in
     and emulator); returns the device symbols launched."""
     env = dict(env, DET_EMU_LOG=str(log))
+    # when this test itself runs in an xdist worker, the child run must not inherit that worker's name: its controller
+    # would write the per-worker log of its own worker of the same name (empty), racing with it
+    for k in [k for k in env if k.startswith('PYTEST_XDIST')]:
+        del env[k]
     par = ['-n', str(workers)] if workers > 1 else []
     r = subprocess.run([sys.executable, '-m', 'pytest', '-p', 'tests.emulated_hip', '-m', 'gpu', '-q', '-x',
                         '-p', 'no:cacheprovider', *par, *ids], cwd=ROOT, env=env, capture_output=True, text=True,
@@ -76,11 +83,14 @@ def launched(names, part):
 
 def test_gpu_tests_through_the_library(emu_env, tmp_path):
     names = run_selected(emu_env, SELECTED, tmp_path / 'kernels', workers=4)
-    for k in ('k_decodeILi', 'k_decode_ms', 'k_prefill2', 'k_repackE', 'k_repack_pf', 'k_qrow', 'k_quantize',
+    for k in ('k_decodeILi', 'k_decode_ms', 'k_prefill2', 'k_repackE', 'k_qrow', 'k_quantize',
               'k_attn', 'k_gdn', 'k_argmax'):
         assert launched(names, k), (k, names)
+    # without DET_PREFILL=streamk no linear carries prefill planes, so their repack never runs
+    assert not launched(names, 'k_repack_pf'), names
 
 
 def test_streamk_prefill_through_the_library(emu_env, tmp_path):
     names = run_selected(dict(emu_env, DET_PREFILL='streamk'), STREAMK, tmp_path / 'kernels')
     assert launched(names, 'k_prefillILi') and not launched(names, 'k_prefill2'), names
+    assert launched(names, 'k_repack_pf'), names

@@ -20,7 +20,7 @@ import pytest
 import oracle
 from tests import gfx950_emu as E
 from tests import isa_waits
-from tests.helpers import same_f32
+from tests.helpers import TIE_GROUPS, same_f32, tie_group
 from tests.test_prefill_emulation import build_planes
 
 GROUP = 128
@@ -437,13 +437,16 @@ def test_ffn_decode_path(qasm):
 @pytest.mark.parametrize('bits', [4, 6, 8])
 def test_quantize_rows(qasm, bits):
     """k_quantize (binary64 scale search, indexed-register code packing) against the oracle's quantize_rows, byte for
-    byte, on Gaussian rows with a zero group, a scaled group and a single outlier."""
+    byte, on Gaussian rows with a zero group, a scaled group, a single outlier and (W4, W6) a group whose scale search
+    ties."""
     rng = np.random.default_rng(80 + bits)
     N, K = 6, 512
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     w[1, 128:256] = 0
     w[2, :128] *= 1e-3
     w[3, 300] = 1.5
+    if bits in TIE_GROUPS:
+        w[4, 128:256] = tie_group(bits, 2.0 ** -12)     # two candidates of equal least error: the first must win
     mem = E.Memory()
     w_d = mem.alloc(w.nbytes, w)
     rb = K // 32 * BPL[bits] + 4 + 2 * (K // GROUP)

@@ -19,6 +19,7 @@ import pytest
 
 import oracle
 from oracle import spec_np
+from tests.helpers import TIE_GROUPS, tie_group
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden', 'quantized_linear.npz')
 
@@ -406,6 +407,42 @@ def test_scale_search_random_groups_against_exact_brute_force():
             assert chosen_step(w, bits) == best
             checked += 1
     assert checked > 100
+
+
+def f64_sse(w, bits, step):
+    """The squared error of candidate `step` as quantize.rs:40-49 computes it: binary64, summed in element order."""
+    qmax = (1 << (bits - 1)) - 1
+    wd = [float(v) for v in np.asarray(w, np.float32)]
+    base = max(abs(v) for v in wd) / qmax
+    s = base * (0.80 + 0.02 * step)
+    err = 0.0
+    for v in wd:
+        q = max(-qmax, min(qmax, round(v / s)))
+        err += (q * s - v) * (q * s - v)
+    return err
+
+
+@pytest.mark.parametrize('bits', [4, 6])
+@pytest.mark.parametrize('scale', [1.0, 2.0 ** -12])
+def test_scale_search_tie_takes_the_first(bits, scale):
+    """Two candidates with identical least error, exactly and in binary64: the strict < keeps the earlier one
+    (quantize.rs:50-52).  A <= comparison, or a search that runs from step 10 down, picks the later step and fails."""
+    (first, second), _ = TIE_GROUPS[bits]
+    w = tie_group(bits, scale)
+    exact = [exact_sse(w, bits, k) for k in range(11)]
+    assert exact[first] == exact[second] == min(exact)
+    assert sorted(exact).count(min(exact)) == 2
+    f64 = [f64_sse(w, bits, k) for k in range(11)]
+    assert f64[first] == f64[second] == min(f64)
+    assert chosen_step(w, bits) == first
+    # the two choices store different c (one group per row: c = f32(s / 65535), m = 65535), so a byte comparison of
+    # rows also tells them apart
+    qmax = (1 << (bits - 1)) - 1
+    base = float(np.abs(w).max()) / qmax
+    c_first, c_second = (np.float32(base * (0.80 + 0.02 * k) / 65535.0) for k in (first, second))
+    assert c_first != c_second
+    row = oracle.quantize_rows(w.reshape(1, 128), bits)[0]
+    assert row[128 * bits // 8:][:4].view('<f4')[0] == c_first
 
 
 def test_scale_search_zero_group():

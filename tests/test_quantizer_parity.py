@@ -1,11 +1,13 @@
 """det_quantize_rows (GPU, binary64) against the oracle's quantize_rows (quantize.rs:33-100), byte for byte,
 and the repack round trip of det_linear_repack."""
+import os
+
 import numpy as np
 import pytest
 
 import oracle
 from det_amd import ffi
-from tests.helpers import gaussian_weights
+from tests.helpers import gaussian_weights, tie_group
 
 pytestmark = pytest.mark.gpu
 
@@ -20,6 +22,20 @@ def test_quantizer_bytes(bits, N, K):
     got = ffi.quantize_rows(ffi.Buf.upload(w), N, K, bits).download()
     bad = np.flatnonzero((want != got).any(axis=1))
     assert bad.size == 0, f'{bad.size} rows differ, first {bad[0]}'
+
+
+@pytest.mark.parametrize('bits', [4, 6])
+def test_quantizer_tie_takes_the_first(bits):
+    """Groups whose scale search ties between two candidates (quantize.rs:50-52, strict <: the first wins), alone
+    and inside a Gaussian row, byte for byte against the oracle."""
+    w = gaussian_weights(91 + bits, 3, 384)
+    w[0] = 0.0
+    w[0, :128] = tie_group(bits)
+    w[1, 256:] = tie_group(bits, 2.0 ** -12)
+    w[2, 128:256] = tie_group(bits, 2.0 ** -20)
+    want = oracle.quantize_rows(w, bits)
+    got = ffi.quantize_rows(ffi.Buf.upload(w), 3, 384, bits).download()
+    assert (want == got).all()
 
 
 def test_quantizer_kat():
@@ -44,7 +60,7 @@ def test_repack_layout(bits):
     G, GB = K // 128, 4 * {8: 32, 6: 24, 4: 16}[bits]
     T = 2 * ((N + 127) // 128)
     nc = K // 32 * {8: 32, 6: 24, 4: 16}[bits]
-    planes = wq[:wq.size // 2].reshape(T, G, GB // 16, 64, 16)
+    planes = wq[:T * G * GB * 64].reshape(T, G, GB // 16, 64, 16)
     for n in range(T * 64):
         t, r = divmod(n, 64)
         got = planes[t, :, :, r, :].reshape(-1)
@@ -77,6 +93,8 @@ def pf_unpack(words, bits):
     return np.concatenate(out).astype(np.int64)
 
 
+@pytest.mark.skipif(os.environ.get('DET_PREFILL') != 'streamk',
+                    reason='the prefill planes exist only when DET_PREFILL=streamk selects the kernel that reads them')
 @pytest.mark.parametrize('bits', [4, 6, 8])
 def test_prefill_planes(bits):
     """det_linear_repack's prefill planes (after the decode tiles): per 32-row block and group, lane l (row l % 32,
@@ -90,7 +108,7 @@ def test_prefill_planes(bits):
     G = K // 128
     NP, SH = {8: (4, 0), 6: (3, 2), 4: (2, 4)}[bits]
     nb32 = 4 * ((N + 127) // 128)
-    pf = wq[wq.size // 2:].reshape(nb32, G, NP, 64, 16)
+    pf = wq[wq.size // 2:].reshape(nb32, G, NP, 64, 16)     # the planes follow the decode tiles (same size)
     nc = K // 32 * {8: 32, 6: 24, 4: 16}[bits]
     codes = np.zeros((nb32 * 32, K), np.int64)
     for n in range(N):
