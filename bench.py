@@ -293,24 +293,49 @@ def write_qwen35_bf16(path, cfg, seed, progress=None):
         head += b''.join(struct.pack('<Q', d) for d in dims) + struct.pack('<IQ', 30 if kind == 'w' else 0, off)
         off += nb + (-nb % 32)
     head += bytes(-len(head) % 32)
-    with open(path, 'wb') as f:
+    # every tensor is drawn in chunks of CHUNK values, chunk j of tensor idx from its own generator [seed, idx, j], so
+    # the chunks can be drawn by a pool of threads (numpy's generators release the GIL) and written in file order
+    CHUNK = 1 << 24
+    jobs = []
+    for idx, ((name, dims, kind), nb) in enumerate(zip(ts, sizes)):
+        n = int(np.prod(dims))
+        for j, lo in enumerate(range(0, n, CHUNK)):
+            jobs.append((idx, j, kind, min(CHUNK, n - lo), lo + CHUNK >= n, nb))
+
+    def draw(job):
+        idx, j, kind, n, last, nb = job
+        a = np.random.default_rng([seed, idx, j]).standard_normal(n, dtype=np.float32) * np.float32(0.02)
+        if kind == 'n':
+            a = a + np.float32(1)
+        elif kind == 'a':
+            a = -np.abs(a) - np.float32(1)
+        data = (a.view(np.uint32) >> 16).astype(np.uint16).tobytes() if kind == 'w' else a.tobytes()
+        return data + (bytes(-nb % 32) if last else b'')
+
+    from concurrent.futures import ThreadPoolExecutor
+    workers = max(1, min(16, os.cpu_count() or 1))
+    with open(path, 'wb') as f, ThreadPoolExecutor(workers) as pool:
         f.write(head)
-        for idx, ((name, dims, kind), nb) in enumerate(zip(ts, sizes)):
-            rng = np.random.default_rng([seed, idx])
-            n = int(np.prod(dims))
-            a = rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)
-            if kind == 'n':
-                a = a + np.float32(1)
-            elif kind == 'a':
-                a = -np.abs(a) - np.float32(1)
-            data = (a.view(np.uint32) >> 16).astype(np.uint16).tobytes() if kind == 'w' else a.tobytes()
-            f.write(data + bytes(-len(data) % 32))
-            if idx % 40 == 0:
-                msg = f'e2e: writing tensor {idx} of {len(ts)}'
-                if progress:
-                    progress(msg)
-                else:
-                    print(msg, file=sys.stderr, flush=True)
+        pending = []
+        for job in jobs:
+            pending.append((job, pool.submit(draw, job)))
+            if len(pending) > 2 * workers:             # bounded memory: at most ~2 chunks per worker in flight
+                done, fut = pending.pop(0)
+                f.write(fut.result())
+                report(done, progress, len(ts))
+        for done, fut in pending:
+            f.write(fut.result())
+            report(done, progress, len(ts))
+
+
+def report(job, progress, nt):
+    idx, j = job[0], job[1]
+    if idx % 40 == 0 and j == 0:
+        msg = f'e2e: writing tensor {idx} of {nt}'
+        if progress:
+            progress(msg)
+        else:
+            print(msg, file=sys.stderr, flush=True)
 
 
 def e2e(args):
