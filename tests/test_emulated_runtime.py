@@ -9,8 +9,8 @@ outputs.  The stand-in reports 4 compute units, so the slicing and stream-K spli
 chip happen at these small shapes.  The stream-K prefill kernel (DET_PREFILL=streamk) runs through the same tests in
 a second process.
 
-Tests that start their own processes (which would not get the stand-in) or whose emulation takes minutes are not in
-the selection; they run on the GPU.
+Tests that start their own processes (unless the child installs the stand-in itself, as the runtime test's does)
+or whose emulation takes minutes are not in the selection; they run on the GPU.
 """
 import os
 import shutil
@@ -25,7 +25,7 @@ ROOT = emulated_hip.ROOT
 HIPCC = os.path.join(os.environ.get('ROCM_PATH', '/opt/rocm'), 'bin', 'hipcc')
 
 SELECTED = [
-    'tests/test_runtime.py::test_malloc_zero_fill_and_accounting',
+    'tests/test_runtime.py',
     'tests/test_prim_parity.py',
     'tests/test_quant_parity.py::test_conformance_norms',
     'tests/test_quant_parity.py::test_scale_underflow_rows',

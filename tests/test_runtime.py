@@ -35,8 +35,11 @@ def test_malloc_zero_fill_and_accounting():
 
 def test_free_of_a_foreign_pointer_aborts():
     code = textwrap.dedent(f'''
-        import sys, ctypes
+        import os, sys, ctypes
         sys.path.insert(0, {ROOT!r})
+        if os.environ.get('DET_EMU_SHIM'):      # run on the CPU emulator when the parent does
+            from tests import emulated_hip
+            emulated_hip.install()
         from det_amd import ffi
         L = ffi.lib()
         p = L.det_malloc(64)
