@@ -29,6 +29,8 @@ compiles to something new fails loudly rather than running on a guess.
 import re
 from fractions import Fraction
 
+import os
+
 import numpy as np
 
 MASK32 = 0xFFFFFFFF
@@ -2092,6 +2094,23 @@ class Workgroup:
                 w.pending_v[r] -= 1
                 w.v[r][p.mask] = p.data[p.mask, k]
 
+    def exec_one(self, w):
+        """One instruction of wave w."""
+        ins = self.prog.instrs[w.pc]
+        if w.gpr_idx is not None and ins.mn.startswith('v_'):
+            ins = indexed(ins, *w.gpr_idx)
+        try:
+            ins.fn(w, ins)
+        except EmuError as e:
+            if ' pc ' in str(e):
+                raise
+            raise EmuError(f'workgroup {self.wg_ids} wave {w.wid} pc {w.pc} ({ins.text}): {e}') from None
+        except Exception as e:
+            raise EmuError(f'wave {w.wid} pc {w.pc} ({ins.text}): {type(e).__name__}: {e}') from e
+        if TRACE is not None:
+            TRACE(w, ins)
+        w.pc += 1
+
     def run(self, max_steps=50_000_000):
         steps = 0
         while True:
@@ -2101,20 +2120,7 @@ class Workgroup:
             progressed = False
             for w in live:
                 while not w.done and not w.at_barrier:
-                    ins = self.prog.instrs[w.pc]
-                    if w.gpr_idx is not None and ins.mn.startswith('v_'):
-                        ins = indexed(ins, *w.gpr_idx)
-                    try:
-                        ins.fn(w, ins)
-                    except EmuError as e:
-                        if ' pc ' in str(e):
-                            raise
-                        raise EmuError(f'workgroup {self.wg_ids} wave {w.wid} pc {w.pc} ({ins.text}): {e}') from None
-                    except Exception as e:
-                        raise EmuError(f'wave {w.wid} pc {w.pc} ({ins.text}): {type(e).__name__}: {e}') from e
-                    if TRACE is not None:
-                        TRACE(w, ins)
-                    w.pc += 1
+                    self.exec_one(w)
                     steps += 1
                     progressed = True
                     if steps > max_steps:
@@ -2125,6 +2131,27 @@ class Workgroup:
                     w.at_barrier = False
             elif not progressed:
                 raise EmuError('deadlock: waves wait at a barrier that others never reach')
+
+    def step(self, rng, budget):
+        """Up to `budget` instructions of this workgroup, its waves taking turns of 1 to 16 instructions in an order
+        drawn from rng; returns (instructions run, finished)."""
+        steps = 0
+        while steps < budget:
+            live = [w for w in self.waves if not w.done]
+            if not live:
+                return steps, True
+            runnable = [w for w in live if not w.at_barrier]
+            if not runnable:                    # every live wave has reached the barrier: release it
+                for w in live:
+                    w.at_barrier = False
+                continue
+            w = runnable[rng.randrange(len(runnable))]
+            for _ in range(rng.randint(1, 16)):
+                if w.done or w.at_barrier or steps >= budget:
+                    break
+                self.exec_one(w)
+                steps += 1
+        return steps, all(w.done for w in self.waves)
 
 
 def indexed(ins, idx, which):
@@ -2174,10 +2201,41 @@ def launch(prog, mem, grid, block, kernarg_bytes, dyn_lds=0):
         ka[off:off + size] = np.frombuffer(int(v).to_bytes(size, 'little'), np.uint8)
     steps = 0
     try:
-        for z in range(gz):
-            for y in range(gy):
-                for x in range(gx):
-                    steps += Workgroup(prog, mem, x, block, y, dyn_lds, z, kernarg=kbase).run()
+        if INTERLEAVE is None:
+            for z in range(gz):
+                for y in range(gy):
+                    for x in range(gx):
+                        steps += Workgroup(prog, mem, x, block, y, dyn_lds, z, kernarg=kbase).run()
+        else:
+            # every workgroup resident at once, run in turns of random length in a random order, so that the
+            # cross-workgroup hand-overs (last arriver of a split tile or K-slice) meet other arrival orders than
+            # the grid order; loads take memory as it is when they issue, stores are visible at once
+            steps = run_interleaved([Workgroup(prog, mem, x, block, y, dyn_lds, z, kernarg=kbase)
+                                     for z in range(gz) for y in range(gy) for x in range(gx)], INTERLEAVE)
     finally:
         mem.release(kbase)
     return steps
+
+
+def run_interleaved(wgs, seed, max_steps=None):
+    """Runs the workgroups all resident at once: a random one (seeded) runs a turn of 1 to 400 instructions, its waves
+    taking sub-turns in random order, until every workgroup has ended; returns the instructions run."""
+    import random
+    rng = random.Random(seed)
+    live = list(wgs)
+    limit = max_steps or 50_000_000 * max(1, len(live) // 64)
+    steps = 0
+    while live:
+        k = rng.randrange(len(live))
+        n, finished = live[k].step(rng, rng.randint(1, 400))
+        steps += n
+        if finished:
+            live.pop(k)
+        if steps > limit:
+            raise EmuError('step limit: the kernel does not end')
+    return steps
+
+
+# None: workgroups run one after another in grid order.  An integer: they are interleaved (seeded by it), see launch.
+# The environment's DET_EMU_INTERLEAVE sets it for a whole test run.
+INTERLEAVE = int(os.environ['DET_EMU_INTERLEAVE']) if os.environ.get('DET_EMU_INTERLEAVE') else None

@@ -151,3 +151,37 @@ def test_fma_rounds_once():
     got = E.exact_fma(np.full(64, 4097.0, np.float32), np.full(64, 4101.0, np.float32),
                       np.zeros(64, np.float32), np.float32)
     assert got[0] == np.float32(2 ** 24 + 24580)                 # the tie itself goes to even: down
+
+
+def arrival_order(seed):
+    """Eight one-lane workgroups each take a ticket from a shared counter (atomic add returning the old value) after a
+    few instructions of other work, and store it at their own slot: the tickets give the arrival order."""
+    mem = E.Memory()
+    cnt = mem.alloc(4, np.zeros(1, np.uint32))
+    out = mem.alloc(32, np.zeros(8, np.uint32))
+    lines = addr_lines(cnt) + ['v_mov_b32 v4, 1'] + ['v_add_u32 v9, v9, v4'] * 20 + [
+        'global_atomic_add v5, v[2:3], v4, off sc0', 's_waitcnt vmcnt(0)',
+        f'v_mov_b32 v7, {out & 0xFFFFFFFF:#x}', f'v_mov_b32 v8, {out >> 32:#x}',
+        'v_lshlrev_b32 v6, 2, s2', 'v_add_co_u32 v7, vcc, v7, v6', 'v_addc_co_u32 v8, vcc, v8, 0, vcc',
+        'global_store_dword v[7:8], v5, off', 's_waitcnt vmcnt(0)', 's_endpgm']
+    prog = E.Program.from_lines(lines)
+    wgs = []
+    for g in range(8):
+        wg = E.Workgroup(prog, mem, g, 1)
+        wg.waves[0].s[2] = g
+        wgs.append(wg)
+    if seed is None:
+        for wg in wgs:
+            wg.run()
+    else:
+        E.run_interleaved(wgs, seed)
+    return [int(v) for v in mem.array(out, np.uint32, 8)]
+
+
+def test_interleaved_workgroups_arrive_in_other_orders():
+    """Run one after another, workgroup g arrives g-th; interleaved, the arrival orders differ from the grid order and
+    from each other, while every workgroup still arrives exactly once (the hand-over tests rely on both)."""
+    assert arrival_order(None) == list(range(8))
+    orders = {tuple(arrival_order(seed)) for seed in range(6)}
+    assert all(sorted(o) == list(range(8)) for o in orders)
+    assert len(orders - {tuple(range(8))}) >= 4

@@ -347,6 +347,44 @@ def test_decode_ms_matches_oracle(asm, bits, M, cus):
     assert d is None, (TS, KS, P, d)
 
 
+# ------------------------------------------------------------------ cross-workgroup hand-overs, interleaved
+# The kernels above that split work between workgroups (k_prefill's split tiles, k_prefill2's K-slices, k_decode's
+# K-split atomics, k_decode_ms's K-slice planes) hand partial sums to whichever workgroup arrives last.  Run one after
+# another, the last in grid order always finishes; here every workgroup is resident at once and they run in seeded
+# random turns (gfx950_emu.run_interleaved), so other workgroups finish, partials are read while their neighbours are
+# still mid-flight and the counters see every arrival order.
+@pytest.fixture
+def interleaved(request):
+    old = E.INTERLEAVE
+    E.INTERLEAVE = request.param
+    yield request.param
+    E.INTERLEAVE = old
+
+
+@pytest.mark.parametrize('interleaved', [7, 8], indirect=True)
+@pytest.mark.parametrize('case', ['prefill_split', 'prefill_xcd', 'prefill2_ks', 'decode_ks', 'decode_ms_ks'])
+def test_hand_overs_interleaved(asm, interleaved, case):
+    if case == 'prefill_split':
+        test_prefill_matches_oracle(asm, 6)
+    elif case == 'prefill_xcd':
+        test_prefill_xcd_remap(asm)
+    elif case == 'prefill2_ks':
+        test_prefill2_widths_and_k_slices(asm, 6, 8)
+    elif case == 'decode_ks':
+        test_decode_matches_oracle(asm, 6, 1, 16)
+    else:                                      # 64 tokens, 32 groups at 16 CUs: two K-slice planes per tile
+        rng = oracle.Rng(77)
+        bits, N, K, M = 6, 72, 4096, 64
+        rows = rng.fake_rows(bits, N, K)
+        xq, sx, mx = oracle.quant(rng.acts_x(M, K))
+        mem = E.Memory()
+        lin = repack(asm, mem, rows, N, K, bits)
+        got, TS, KS, P = run_decode_ms(asm, mem, lin, N, K, bits, xq, sx, mx, M, 16)
+        assert KS == 2
+        d = same_f32(oracle.gemm(rows, N, K, bits, xq, sx, mx), got)
+        assert d is None, (TS, KS, P, d)
+
+
 # ------------------------------------------------------------------ activation quantization and the FFN decode path
 def run_qrow(asm, mem, mode, a, b=None, eps=0.0, w_y=False):
     """launch_qrow: k_qrow<MODE, EPT> over M rows of n (group mode, 16-byte aligned buffers)."""
