@@ -203,10 +203,14 @@ impl Backend for Hip {
         let (k, bits) = (rows.k, rows.bits);
         let n: usize = rows.widths.iter().sum();
         let row_bytes = crate::spec::det_row_bytes(bits, k);
-        let staging = device::<u8>(n * row_bytes);
+        // one host image of the rows, one copy to the device (a copy per row would cost a round trip per row)
+        let mut image = Vec::with_capacity(n * row_bytes);
         for r in 0..n {
-            unsafe { to_device(staging.ptr_at(r * row_bytes), rows.row(r).as_ptr(), row_bytes) };
+            image.extend_from_slice(&rows.row(r)[..row_bytes]);
         }
+        let staging = device::<u8>(image.len());
+        unsafe { to_device(staging.as_mut_ptr(), image.as_ptr(), image.len()) };
+        drop(image);
         let (mut wq_bytes, mut c_bytes, mut m_bytes) = (0usize, 0usize, 0usize);
         unsafe { sys::hip::det_linear_sizes(ci(n), ci(k), bits as c_int, &mut wq_bytes, &mut c_bytes, &mut m_bytes) };
         let planes = (device::<u8>(wq_bytes), device::<f32>(c_bytes / 4), device::<u16>(m_bytes / 2));
