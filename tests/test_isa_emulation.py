@@ -361,8 +361,9 @@ def interleaved(request):
     E.INTERLEAVE = old
 
 
-@pytest.mark.parametrize('interleaved', [7, 8], indirect=True)
-@pytest.mark.parametrize('case', ['prefill_split', 'prefill_xcd', 'prefill2_ks', 'decode_ks', 'decode_ms_ks'])
+@pytest.mark.parametrize('case,interleaved', [('prefill_split', 7), ('prefill_split', 8), ('prefill_xcd', 7),
+                                              ('prefill2_ks', 8), ('decode_ks', 7), ('decode_ms_ks', 8)],
+                         indirect=['interleaved'])
 def test_hand_overs_interleaved(asm, interleaved, case):
     if case == 'prefill_split':
         test_prefill_matches_oracle(asm, 6)
